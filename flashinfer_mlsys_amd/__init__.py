@@ -1,0 +1,192 @@
+"""MI355X-native FP8 block-scale DeepSeek-V3 MoE operator (32 local experts).
+
+Operator ``moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048``
+(``reference moe/ref_moe.json``). The Python entry points keep the reference's
+names and positional order:
+
+* ``kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale,
+  gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
+  local_expert_offset, routed_scaling_factor, output)`` -- destination-passing
+  form of ``solution/triton/kernel.py:292-305``; writes ``output`` in place.
+* ``run(...)`` -- the same ten inputs, returns the bf16 [T, 7168] output, as
+  ``reference moe/ref_moe.py:4-16``.
+
+Both validate the inputs the way ``ref_moe.py:41-63`` does (an
+``AssertionError`` subclass on a geometry or dtype mismatch) and then call the
+hand-written gfx950 HIP kernels in ``libmoe_mi355x.so`` through its C ABI on
+the current HIP stream. There is no CPU or PyTorch fallback: a missing library
+or a CPU tensor raises.
+
+``route`` and ``dispatch`` expose the first two stages for parity tests.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = ["kernel", "run", "route", "dispatch", "workspace_size", "MoEInputError", "set_path"]
+
+H = 7168
+I = 2048
+E_GLOBAL = 256
+E_LOCAL = 32
+BLOCK = 128
+TOP_K = 8
+
+
+class MoEInputError(AssertionError):
+    """An input does not match the operator definition (shape, dtype, device)."""
+
+
+def _req(cond, msg):
+    if not cond:
+        raise MoEInputError(msg)
+
+
+def _on_gpu(t, name):
+    _req(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
+    _req(t.is_cuda, f"{name} must be on a ROCm GPU (got {t.device}); there is no CPU path")
+    return t
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _contig(t):
+    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
+
+
+def workspace_size(T: int) -> int:
+    """Device workspace bytes ``kernel`` needs for T tokens."""
+    return int(_lib.load().moe_fp8_workspace_size(int(T)))
+
+
+def set_path(path: int) -> int:
+    """Expert-GEMM shape: 0 by token count, 1 decode shape, 2 prefill shape. Returns the old value."""
+    r = _lib.load().moe_fp8_set_path(int(path))
+    if r < 0:
+        raise ValueError("path must be 0, 1 or 2")
+    return r
+
+
+def _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale):
+    names = ["routing_logits", "routing_bias", "hidden_states", "hidden_states_scale", "gemm1_weights",
+             "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]
+    ts = [routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+          gemm1_weights_scale, gemm2_weights, gemm2_weights_scale]
+    for t, n in zip(ts, names):
+        _on_gpu(t, n)
+    dev = hidden_states.device
+    for t, n in zip(ts, names):
+        _req(t.device == dev, f"{n} is on {t.device}, expected {dev}")
+    _req(routing_logits.dim() == 2, "routing_logits must be [T, 256]")
+    T = routing_logits.shape[0]
+    _req(routing_logits.shape[1] == E_GLOBAL, "num_experts must be 256")
+    _req(gemm1_weights.dim() == 3 and gemm1_weights.shape[0] == E_LOCAL, "num_local_experts must be 32")
+    _req(hidden_states.shape == (T, H), "hidden_size must be 7168")
+    _req(hidden_states_scale.shape == (H // BLOCK, T), "hidden_states_scale must be [56, T]")
+    _req(gemm1_weights.shape == (E_LOCAL, 2 * I, H), "intermediate_size must be 2048")
+    _req(gemm1_weights_scale.shape == (E_LOCAL, 2 * I // BLOCK, H // BLOCK), "gemm1_weights_scale must be [32, 32, 56]")
+    _req(gemm2_weights.shape == (E_LOCAL, H, I), "gemm2_weights must be [32, 7168, 2048]")
+    _req(gemm2_weights_scale.shape == (E_LOCAL, H // BLOCK, I // BLOCK), "gemm2_weights_scale must be [32, 56, 16]")
+    _req(routing_bias.shape[-1] == E_GLOBAL and routing_bias.numel() == E_GLOBAL, "routing_bias must have 256 entries")
+    _req(routing_logits.dtype == torch.float32, "routing_logits must be float32")
+    _req(routing_bias.dtype == torch.bfloat16, "routing_bias must be bfloat16")
+    _req(hidden_states.dtype == torch.float8_e4m3fn, "hidden_states must be float8_e4m3fn")
+    _req(gemm1_weights.dtype == torch.float8_e4m3fn, "gemm1_weights must be float8_e4m3fn")
+    _req(gemm2_weights.dtype == torch.float8_e4m3fn, "gemm2_weights must be float8_e4m3fn")
+    for t, n in ((hidden_states_scale, "hidden_states_scale"), (gemm1_weights_scale, "gemm1_weights_scale"),
+                 (gemm2_weights_scale, "gemm2_weights_scale")):
+        _req(t.dtype == torch.float32, f"{n} must be float32")
+    return T
+
+
+@torch.no_grad()
+def kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+           routed_scaling_factor, output, workspace=None):
+    """Destination-passing operator: writes bf16 [T, 7168] into ``output``; returns None."""
+    T = _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                  gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
+    _on_gpu(output, "output")
+    _req(output.shape == (T, H) and output.dtype == torch.bfloat16, "output must be bf16 [T, 7168]")
+    _req(output.device == hidden_states.device, "output must be on the inputs' device")
+    if T == 0:
+        return None
+    lib = _lib.load()
+    need = int(lib.moe_fp8_workspace_size(T))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=hidden_states.device)
+    _req(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need, "workspace too small")
+    args = [_contig(t) for t in (routing_logits, routing_bias.reshape(-1), hidden_states, hidden_states_scale,
+                                 gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)]
+    out = output if (output.is_contiguous() and output.data_ptr() % 16 == 0) else torch.empty_like(
+        output, memory_format=torch.contiguous_format)
+    with torch.cuda.device(hidden_states.device):
+        code = lib.moe_fp8_forward(*[a.data_ptr() for a in args], T, int(local_expert_offset),
+                                   float(routed_scaling_factor), out.data_ptr(), workspace.data_ptr(),
+                                   workspace.numel() * workspace.element_size(), _stream(hidden_states.device))
+    _lib.check(code, "moe_fp8_forward")
+    if out is not output:
+        output.copy_(out)
+    return None
+
+
+@torch.no_grad()
+def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+        gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor):
+    """Value-returning operator (``reference moe/ref_moe.py:4-16``): returns bf16 [T, 7168]."""
+    _on_gpu(hidden_states, "hidden_states")
+    T = routing_logits.shape[0]
+    output = torch.empty((T, H), dtype=torch.bfloat16, device=hidden_states.device)
+    kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
+           gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, output)
+    return output
+
+
+@torch.no_grad()
+def route(routing_logits, routing_bias, routed_scaling_factor):
+    """Routing stage: (topk_ids int32 [T, 8] ascending per token, topk_w fp32 [T, 8], tok_pair int32 [T, 8] = -1)."""
+    _on_gpu(routing_logits, "routing_logits")
+    _on_gpu(routing_bias, "routing_bias")
+    _req(routing_logits.dtype == torch.float32 and routing_logits.dim() == 2
+         and routing_logits.shape[1] == E_GLOBAL, "routing_logits must be float32 [T, 256]")
+    _req(routing_bias.dtype == torch.bfloat16 and routing_bias.numel() == E_GLOBAL, "routing_bias must be bf16 [256]")
+    T = routing_logits.shape[0]
+    dev = routing_logits.device
+    ids = torch.empty((T, TOP_K), dtype=torch.int32, device=dev)
+    w = torch.empty((T, TOP_K), dtype=torch.float32, device=dev)
+    pair = torch.empty((T, TOP_K), dtype=torch.int32, device=dev)
+    if T == 0:
+        return ids, w, pair
+    lg, b = _contig(routing_logits), _contig(routing_bias.reshape(-1))
+    with torch.cuda.device(dev):
+        code = _lib.load().moe_fp8_route(lg.data_ptr(), b.data_ptr(), T, float(routed_scaling_factor),
+                                         ids.data_ptr(), w.data_ptr(), pair.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_route")
+    return ids, w, pair
+
+
+@torch.no_grad()
+def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
+    """Dispatch stage: returns (header int32 [128], perm_tok int32 [8T], perm_w fp32 [8T], tok_pair).
+
+    ``header`` holds counts[32], seg_start[33], n_active, active[32]. ``tok_pair``
+    (from ``route``) is updated in place with each local pair's index.
+    """
+    _on_gpu(topk_ids, "topk_ids")
+    T = topk_ids.shape[0]
+    dev = topk_ids.device
+    header = torch.zeros(128, dtype=torch.int32, device=dev)
+    perm_tok = torch.full((max(1, TOP_K * T),), -1, dtype=torch.int32, device=dev)
+    perm_w = torch.zeros((max(1, TOP_K * T),), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        code = _lib.load().moe_fp8_dispatch(topk_ids.data_ptr() if T else None,
+                                            topk_w.data_ptr() if T else None, T, int(local_expert_offset),
+                                            header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
+                                            tok_pair.data_ptr() if T else header.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_dispatch")
+    return header, perm_tok, perm_w, tok_pair

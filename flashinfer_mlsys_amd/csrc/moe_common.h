@@ -1,0 +1,105 @@
+// Shared constants, vector types and device helpers for the FP8 block-scale
+// DeepSeek-V3 MoE kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Fixed operator geometry (reference moe/ref_moe.py:33-54).
+constexpr int H = 7168;            // hidden size
+constexpr int I = 2048;            // intermediate size
+constexpr int N1 = 2 * I;          // gemm1 output width (first half X1, second half X2)
+constexpr int E_GLOBAL = 256;
+constexpr int E_LOCAL = 32;
+constexpr int TOP_K = 8;
+constexpr int N_GROUP = 8;
+constexpr int TOPK_GROUP = 4;
+constexpr int GROUP_SIZE = E_GLOBAL / N_GROUP;  // 32
+constexpr int BLK = 128;           // quantisation block edge
+constexpr int NB_H = H / BLK;      // 56
+constexpr int NB_I = I / BLK;      // 16
+constexpr int NB_N1 = N1 / BLK;    // 32
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// Device-side dispatch header at the start of the workspace.
+struct DispatchHeader {
+  int32_t counts[E_LOCAL];         // tokens per local expert
+  int32_t seg_start[E_LOCAL + 1];  // exclusive scan of counts; seg_start[32] = P
+  int32_t n_active;                // experts with count > 0
+  int32_t active[E_LOCAL];         // their local ids, ascending
+  int32_t pad[256 / 4 * 2 - (E_LOCAL * 3 + 2)];
+};
+static_assert(sizeof(DispatchHeader) == 512, "header is 512 bytes");
+
+// One MFMA over a full 128-wide K block: D(16x16 fp32) = A(16x128 e4m3) * B(128x16 e4m3).
+// Lane l holds row (l % 16) of A / column (l % 16) of B and the 32 K values
+// [32*(l/16), 32*(l/16)+32); the result holds rows 4*(l/16)+r, column l % 16.
+// E8M0 scale 127 is 2^0: block scales are applied in fp32 by the caller.
+__device__ __forceinline__ v4f mfma_fp8_k128(const v8i& a, const v8i& b) {
+  v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
+}
+
+// D += A(16x32 bf16) * B(32x16 bf16); lane l holds row/column l % 16 and
+// K values [8*(l/16), 8*(l/16)+8).
+__device__ __forceinline__ v4f mfma_bf16_k32(const v8bf& a, const v8bf& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Four e4m3 codes (one dword) -> four bf16 packed in two dwords. e4m3 values
+// are exact in fp32 and in bf16 (3 mantissa bits), so taking the upper half of
+// the fp32 pattern is exact.
+template <bool HI>
+__device__ __forceinline__ v2f fp8x2_to_f32(uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+}
+__device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
+  // byte select: result = {hi[31:16], lo[31:16]}
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+__device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& o0, uint32_t& o1) {
+  v2f a = fp8x2_to_f32<false>(w);
+  v2f b = fp8x2_to_f32<true>(w);
+  o0 = pack_bf16_hi(a[0], a[1]);
+  o1 = pack_bf16_hi(b[0], b[1]);
+}
+
+// fp32 -> bf16 bits, round to nearest even (quiet NaN kept NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__host__ __device__ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Workspace layout for T tokens (worst case P = 8T routed pairs).
+struct WorkspaceLayout {
+  size_t hdr, topk_ids, topk_w, tok_pair, perm_tok, perm_w, c_act, partial, total;
+  __host__ __device__ static WorkspaceLayout make(int64_t T) {
+    WorkspaceLayout L;
+    const size_t P = (size_t)T * TOP_K;
+    size_t o = 0;
+    L.hdr = o;      o += align_up(sizeof(DispatchHeader), 256);
+    L.topk_ids = o; o += align_up((size_t)T * TOP_K * 4, 256);
+    L.topk_w = o;   o += align_up((size_t)T * TOP_K * 4, 256);
+    L.tok_pair = o; o += align_up((size_t)T * TOP_K * 4, 256);
+    L.perm_tok = o; o += align_up(P * 4, 256);
+    L.perm_w = o;   o += align_up(P * 4, 256);
+    L.c_act = o;    o += align_up(P * I * 2, 256);
+    L.partial = o;  o += align_up(P * H * 4, 256);
+    L.total = o;
+    return L;
+  }
+};
+
+}  // namespace moe

@@ -1,0 +1,564 @@
+// Grouped expert GEMMs and the ordered combine for the FP8 DeepSeek-V3 MoE.
+//
+// Per local expert e with token segment rows [seg, seg + cnt) (ascending tokens):
+//   GEMM1  G1 = A_e . W13_e^T        [cnt, 7168] x [7168, 4096]  (ref_moe.py:147-153)
+//   SwiGLU C  = X1 * silu(X2)        X1 = G1[:, :2048], X2 = G1[:, 2048:] (ref_moe.py:155-159)
+//   GEMM2  O  = C . W2_e^T           [cnt, 2048] x [2048, 7168]  (ref_moe.py:161-162)
+//   weight O * w[token, e] into one fp32 row per (token, expert) pair
+//   combine: out[t] = sum over t's local experts in ascending id, then bf16 (ref_moe.py:164-168)
+//
+// GEMM1 runs on the e4m3 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
+// scales). One MFMA covers exactly one 128-wide K block, so the fp32 block
+// scales are applied once per block: acc += P * (s_act[row, kb] * s_w[nb, kb]).
+// GEMM2 runs on the bf16 MFMA (16x16x32): e4m3 weights widen to bf16 exactly;
+// the bf16 C keeps the SwiGLU output to 8 significant bits.
+//
+// Two shapes of each GEMM:
+//   *_stream  -- few rows per expert (decode). One workgroup per (active expert,
+//                16-column tile); its waves split K and preload their whole weight
+//                slice into registers, so each weight byte is read once and all
+//                loads are in flight together. Partial sums meet in LDS.
+//   *_tiled   -- many rows per expert (prefill). Persistent workgroups walk a
+//                device-built list of (expert, row tile, column tile) items with
+//                double-buffered LDS tiles; consecutive items share the weight
+//                tile and are kept on one XCD so its L2 serves the repeats.
+#include "moe_common.h"
+
+namespace moe {
+
+__device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
+  const v4i lo = *reinterpret_cast<const v4i*>(p);
+  const v4i hi = *reinterpret_cast<const v4i*>(p + 16);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 in K order.
+__device__ __forceinline__ v8bf fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  v4i r;
+  uint32_t a, b, c, d;
+  fp8x4_to_bf16x4(w0, a, b);
+  fp8x4_to_bf16x4(w1, c, d);
+  r[0] = (int)a; r[1] = (int)b; r[2] = (int)c; r[3] = (int)d;
+  return __builtin_bit_cast(v8bf, r);
+}
+
+__device__ __forceinline__ float silu_mul(float x1, float x2) {
+  return (x2 / (1.0f + expf(-x2))) * x1;
+}
+
+// Workgroup b of G (G a multiple of 8) -> item index such that the G/8
+// workgroups of one XCD (hardware places workgroup b on XCD b % 8) get
+// consecutive indices.
+__device__ __forceinline__ int xcd_remap(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
+
+// ---------------------------------------------------------------------------
+// GEMM1 + SwiGLU, stream shape
+// ---------------------------------------------------------------------------
+constexpr int S1_SPLITK = 8;                   // waves per workgroup, one K slice each
+constexpr int S1_KPW = NB_H / S1_SPLITK;       // 7 K blocks per wave
+constexpr int S1_MT = 2;                       // 16-row tiles per pass
+static_assert(NB_H % S1_SPLITK == 0, "K slices");
+
+__global__ __launch_bounds__(64 * S1_SPLITK) void gemm1_stream_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
+    const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
+  __shared__ float red[S1_SPLITK][S1_MT][2][4][64];
+  const int slot = blockIdx.y;
+  if (slot >= hdr->n_active) return;
+  const int le = hdr->active[slot];
+  const int cnt = hdr->counts[le], seg = hdr->seg_start[le];
+  const int nt = blockIdx.x;  // pair columns [16 nt, 16 nt + 16)
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int kb0 = wave * S1_KPW;
+
+  const uint8_t* wu = w13 + ((size_t)le * N1 + nt * 16 + col) * H + kg * 32;
+  const uint8_t* wg = wu + (size_t)I * H;
+  const float* su = s13 + ((size_t)le * NB_N1 + (nt * 16) / BLK) * NB_H;
+  const float* sg = su + (size_t)NB_I * NB_H;
+  v8i bu[S1_KPW], bg[S1_KPW];
+#pragma unroll
+  for (int kk = 0; kk < S1_KPW; ++kk) {
+    bu[kk] = load_v8i(wu + (kb0 + kk) * BLK);
+    bg[kk] = load_v8i(wg + (kb0 + kk) * BLK);
+  }
+
+  for (int m0 = 0; m0 < cnt; m0 += 16 * S1_MT) {
+    int tok_a[S1_MT], tok_o[S1_MT][4];
+#pragma unroll
+    for (int mt = 0; mt < S1_MT; ++mt) {
+      tok_a[mt] = perm_tok[seg + min(m0 + mt * 16 + col, cnt - 1)];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tok_o[mt][r] = perm_tok[seg + min(m0 + mt * 16 + 4 * kg + r, cnt - 1)];
+    }
+    v4f au[S1_MT], ag[S1_MT];
+#pragma unroll
+    for (int mt = 0; mt < S1_MT; ++mt) { au[mt] = v4f{0.f, 0.f, 0.f, 0.f}; ag[mt] = au[mt]; }
+#pragma unroll
+    for (int kk = 0; kk < S1_KPW; ++kk) {
+      const int kb = kb0 + kk;
+      const float swu = su[kb], swg = sg[kb];
+#pragma unroll
+      for (int mt = 0; mt < S1_MT; ++mt) {
+        const v8i a = load_v8i(hidden + (size_t)tok_a[mt] * H + kb * BLK + kg * 32);
+        const v4f pu = mfma_fp8_k128(a, bu[kk]);
+        const v4f pg = mfma_fp8_k128(a, bg[kk]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sa = hscale[(size_t)kb * T + tok_o[mt][r]];
+          au[mt][r] += pu[r] * (sa * swu);
+          ag[mt][r] += pg[r] * (sa * swg);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < S1_MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        red[wave][mt][0][r][lane] = au[mt][r];
+        red[wave][mt][1][r][lane] = ag[mt][r];
+      }
+    __syncthreads();
+    {
+      static_assert(S1_MT * 4 * 64 == 64 * S1_SPLITK, "one output per thread");
+      const int mt = tid >> 8, r = (tid >> 6) & 3, ln = tid & 63;
+      float x1 = 0.f, x2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < S1_SPLITK; ++w) {
+        x1 += red[w][mt][0][r][ln];
+        x2 += red[w][mt][1][r][ln];
+      }
+      const int row = m0 + mt * 16 + 4 * (ln >> 4) + r;
+      if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 16 + (ln & 15)] = f32_to_bf16_rne(silu_mul(x1, x2));
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM2 (+ routing weight), stream shape
+// ---------------------------------------------------------------------------
+constexpr int S2_SPLITK = 4;
+constexpr int S2_KPW = NB_I / S2_SPLITK;  // 4 K blocks per wave
+constexpr int S2_MT = 2;
+
+__global__ __launch_bounds__(64 * S2_SPLITK) void gemm2_stream_kernel(
+    const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+  __shared__ float red[S2_SPLITK][S2_MT][4][64];
+  const int slot = blockIdx.y;
+  if (slot >= hdr->n_active) return;
+  const int le = hdr->active[slot];
+  const int cnt = hdr->counts[le], seg = hdr->seg_start[le];
+  const int nt = blockIdx.x;  // output columns [16 nt, 16 nt + 16)
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int kb0 = wave * S2_KPW;
+
+  const uint8_t* wrow = w2 + ((size_t)le * H + nt * 16 + col) * I + kg * 32;
+  const float* sw = s2 + ((size_t)le * NB_H + (nt * 16) / BLK) * NB_I;
+  v8i raw[S2_KPW];
+#pragma unroll
+  for (int kk = 0; kk < S2_KPW; ++kk) raw[kk] = load_v8i(wrow + (kb0 + kk) * BLK);
+
+  for (int m0 = 0; m0 < cnt; m0 += 16 * S2_MT) {
+    const uint16_t* arow[S2_MT];
+#pragma unroll
+    for (int mt = 0; mt < S2_MT; ++mt)
+      arow[mt] = c_act + (size_t)(seg + min(m0 + mt * 16 + col, cnt - 1)) * I + kg * 32;
+    v4f acc[S2_MT];
+#pragma unroll
+    for (int mt = 0; mt < S2_MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < S2_KPW; ++kk) {
+      const int kb = kb0 + kk;
+      const float s = sw[kb];
+      v8bf b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = fp8x8_to_bf16x8((uint32_t)raw[kk][2 * j], (uint32_t)raw[kk][2 * j + 1]);
+#pragma unroll
+      for (int mt = 0; mt < S2_MT; ++mt) {
+        v4f p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v8bf a = *reinterpret_cast<const v8bf*>(arow[mt] + kb * BLK + 8 * j);
+          p = mfma_bf16_k32(a, b[j], p);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][r] += p[r] * s;
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < S2_MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][mt][r][lane] = acc[mt][r];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < (S2_MT * 4 * 64) / (64 * S2_SPLITK); ++q) {
+      const int o = tid + q * 64 * S2_SPLITK;
+      const int mt = o >> 8, r = (o >> 6) & 3, ln = o & 63;
+      float x = 0.f;
+#pragma unroll
+      for (int w = 0; w < S2_SPLITK; ++w) x += red[w][mt][r][ln];
+      const int row = m0 + mt * 16 + 4 * (ln >> 4) + r;
+      if (row < cnt) partial[(size_t)(seg + row) * H + nt * 16 + (ln & 15)] = x * perm_w[seg + row];
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Shared item list for the tiled kernels: every workgroup rebuilds the
+// per-expert row-tile prefix from the dispatch header (32 values).
+// ---------------------------------------------------------------------------
+struct TileMap {
+  int mt_prefix[E_LOCAL + 1];
+  int cnt[E_LOCAL];
+  int seg[E_LOCAL];
+};
+
+template <int BM>
+__device__ __forceinline__ void build_tile_map(const DispatchHeader* hdr, TileMap& m) {
+  const int tid = threadIdx.x;
+  if (tid < E_LOCAL) {
+    m.cnt[tid] = hdr->counts[tid];
+    m.seg[tid] = hdr->seg_start[tid];
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e < E_LOCAL; ++e) {
+      m.mt_prefix[e] = acc;
+      acc += (m.cnt[e] + BM - 1) / BM;
+    }
+    m.mt_prefix[E_LOCAL] = acc;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
+  int e = 0;
+  while (m.mt_prefix[e + 1] <= mg) ++e;
+  return e;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM1 + SwiGLU, tiled shape: 128 rows x 64 pair columns (128 W13 rows) per item.
+// 4 waves as 2 (rows) x 2 (pair columns); each wave 64 rows x 32 pair columns.
+// ---------------------------------------------------------------------------
+constexpr int T1_BM = 128;
+constexpr int T1_BNP = 64;
+constexpr int T1_LDS = 144;  // bytes per staged 128-byte K row (+16 keeps 16 rows on distinct banks)
+constexpr int T1_NT = I / T1_BNP;
+
+__global__ __launch_bounds__(256, 2) void gemm1_tiled_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
+    const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][T1_BM * T1_LDS];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][2 * T1_BNP * T1_LDS];
+  __shared__ __attribute__((aligned(16))) float sSa[2][T1_BM];
+  __shared__ int sTok[T1_BM];
+  __shared__ TileMap map;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int fr = lane & 15, kg = lane >> 4;
+  build_tile_map<T1_BM>(hdr, map);
+  const int total_m = map.mt_prefix[E_LOCAL];
+  const int total = total_m * T1_NT;
+
+  for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
+    const int nt = item / total_m, mg = item % total_m;
+    const int e = find_expert(map, mg);
+    const int m0 = (mg - map.mt_prefix[e]) * T1_BM;
+    const int cnt = map.cnt[e], seg = map.seg[e];
+    const int valid = min(T1_BM, cnt - m0);
+    if (tid < T1_BM) sTok[tid] = perm_tok[seg + m0 + min(tid, valid - 1)];
+    __syncthreads();
+
+    const uint8_t* a_src[4];
+    const uint8_t* b_src[4];
+    int lds_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      a_src[i] = hidden + (size_t)sTok[row] * H + ch * 16;
+      const int wr = row < T1_BNP ? nt * T1_BNP + row : I + nt * T1_BNP + (row - T1_BNP);
+      b_src[i] = w13 + ((size_t)e * N1 + wr) * H + ch * 16;
+      lds_off[i] = row * T1_LDS + ch * 16;
+    }
+    const int my_tok = tid < T1_BM ? sTok[tid] : 0;
+    const float* su = s13 + ((size_t)e * NB_N1 + (nt * T1_BNP) / BLK) * NB_H;
+    const float* sg = s13 + ((size_t)e * NB_N1 + (I + nt * T1_BNP) / BLK) * NB_H;
+
+    v4i ra[4], rb[4];
+    float rsa = 0.f;
+    auto gload = [&](int kb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ra[i] = *reinterpret_cast<const v4i*>(a_src[i] + kb * BLK);
+        rb[i] = *reinterpret_cast<const v4i*>(b_src[i] + kb * BLK);
+      }
+      if (tid < T1_BM) rsa = hscale[(size_t)kb * T + my_tok];
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<v4i*>(&sA[buf][lds_off[i]]) = ra[i];
+        *reinterpret_cast<v4i*>(&sB[buf][lds_off[i]]) = rb[i];
+      }
+      if (tid < T1_BM) sSa[buf][tid] = rsa;
+    };
+
+    v4f accu[4][2], accg[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < NB_H; ++kb) {
+      const int buf = kb & 1;
+      if (kb + 1 < NB_H) gload(kb + 1);
+      const float swu = su[kb], swg = sg[kb];
+      v8i a[4], bu[2], bg[2];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) a[mt] = load_v8i(&sA[buf][(wm * 64 + mt * 16 + fr) * T1_LDS + kg * 32]);
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2) {
+        bu[n2] = load_v8i(&sB[buf][(wn * 32 + n2 * 16 + fr) * T1_LDS + kg * 32]);
+        bg[n2] = load_v8i(&sB[buf][(T1_BNP + wn * 32 + n2 * 16 + fr) * T1_LDS + kg * 32]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const v4f sa = *reinterpret_cast<const v4f*>(&sSa[buf][wm * 64 + mt * 16 + 4 * kg]);
+        v4f fu, fg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
+#pragma unroll
+        for (int n2 = 0; n2 < 2; ++n2) {
+          const v4f pu = mfma_fp8_k128(a[mt], bu[n2]);
+          const v4f pg = mfma_fp8_k128(a[mt], bg[n2]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            accu[mt][n2][r] += pu[r] * fu[r];
+            accg[mt][n2][r] += pg[r] * fg[r];
+          }
+        }
+      }
+      if (kb + 1 < NB_H) lstore(buf ^ 1);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * 64 + mt * 16 + 4 * kg + r;
+          if (row < cnt) {
+            const int col = nt * T1_BNP + wn * 32 + n2 * 16 + fr;
+            c_act[(size_t)(seg + row) * I + col] = f32_to_bf16_rne(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
+          }
+        }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM2 (+ routing weight), tiled shape: 128 rows x 128 output columns per item,
+// K staged 64 at a time (half a scale block). 4 waves as 2 x 2 of 64 x 64.
+// ---------------------------------------------------------------------------
+constexpr int T2_BM = 128;
+constexpr int T2_BN = 128;
+constexpr int T2_BK = 64;
+constexpr int T2_LDS = 144;  // bytes per staged row of 64 bf16 (+16)
+constexpr int T2_NT = H / T2_BN;
+constexpr int T2_NK = I / T2_BK;  // 32 stages
+
+__global__ __launch_bounds__(256, 2) void gemm2_tiled_kernel(
+    const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][T2_BM * T2_LDS];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][T2_BN * T2_LDS];
+  __shared__ TileMap map;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int fr = lane & 15, kg = lane >> 4;
+  build_tile_map<T2_BM>(hdr, map);
+  const int total_m = map.mt_prefix[E_LOCAL];
+  const int total = total_m * T2_NT;
+
+  for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
+    const int nt = item / total_m, mg = item % total_m;
+    const int e = find_expert(map, mg);
+    const int m0 = (mg - map.mt_prefix[e]) * T2_BM;
+    const int cnt = map.cnt[e], seg = map.seg[e];
+
+    const uint8_t* a_src[4];
+    int a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int r = seg + min(m0 + row, cnt - 1);
+      a_src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)r * I) + ch * 16;
+      a_off[i] = row * T2_LDS + ch * 16;
+    }
+    const uint8_t* b_src[2];
+    int b_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i, row = c >> 2, ch = c & 3;
+      b_src[i] = w2 + ((size_t)e * H + nt * T2_BN + row) * I + ch * 16;
+      b_off[i] = row * T2_LDS + ch * 32;
+    }
+    const float* sw = s2 + ((size_t)e * NB_H + (nt * T2_BN) / BLK) * NB_I;
+
+    v4i ra[4], rb[2];
+    auto gload = [&](int kk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const v4i*>(a_src[i] + kk * T2_BK * 2);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const v4i*>(b_src[i] + kk * T2_BK);
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&sA[buf][a_off[i]]) = ra[i];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const v8bf lo = fp8x8_to_bf16x8((uint32_t)rb[i][0], (uint32_t)rb[i][1]);
+        const v8bf hi = fp8x8_to_bf16x8((uint32_t)rb[i][2], (uint32_t)rb[i][3]);
+        *reinterpret_cast<v8bf*>(&sB[buf][b_off[i]]) = lo;
+        *reinterpret_cast<v8bf*>(&sB[buf][b_off[i] + 16]) = hi;
+      }
+    };
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int n4 = 0; n4 < 4; ++n4) acc[mt][n4] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kk = 0; kk < T2_NK; ++kk) {
+      const int buf = kk & 1;
+      if (kk + 1 < T2_NK) gload(kk + 1);
+      const float s = sw[kk >> 1];
+      v8bf a[4][2], b[4][2];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          a[mt][j] = *reinterpret_cast<const v8bf*>(&sA[buf][(wm * 64 + mt * 16 + fr) * T2_LDS + kg * 32 + j * 16]);
+#pragma unroll
+      for (int n4 = 0; n4 < 4; ++n4)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          b[n4][j] = *reinterpret_cast<const v8bf*>(&sB[buf][(wn * 64 + n4 * 16 + fr) * T2_LDS + kg * 32 + j * 16]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int n4 = 0; n4 < 4; ++n4) {
+          v4f p = {0.f, 0.f, 0.f, 0.f};
+          p = mfma_bf16_k32(a[mt][0], b[n4][0], p);
+          p = mfma_bf16_k32(a[mt][1], b[n4][1], p);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][n4][r] += p[r] * s;
+        }
+      if (kk + 1 < T2_NK) lstore(buf ^ 1);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + mt * 16 + 4 * kg + r;
+        if (row < cnt) {
+          const float w = perm_w[seg + row];
+          float* dst = partial + (size_t)(seg + row) * H + nt * T2_BN + wn * 64 + fr;
+#pragma unroll
+          for (int n4 = 0; n4 < 4; ++n4) dst[n4 * 16] = acc[mt][n4][r] * w;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Ordered combine: out[t] = bf16( sum_j partial[pair(t, j)] ) over t's local
+// experts in ascending id; zeros for tokens with none.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
+                                                      const int32_t* __restrict__ tok_pair, int T,
+                                                      uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  int p[TOP_K];
+#pragma unroll
+  for (int j = 0; j < TOP_K; ++j) p[j] = tok_pair[(size_t)t * TOP_K + j];
+#pragma unroll
+  for (int i = 0; i < H / 1024; ++i) {
+    const int h = i * 1024 + threadIdx.x * 4;
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < TOP_K; ++j) {
+      if (p[j] >= 0) {
+        const float4 v = *reinterpret_cast<const float4*>(partial + (size_t)p[j] * H + h);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+      }
+    }
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+    o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+    *reinterpret_cast<uint2*>(out + (size_t)t * H + h) = o;
+  }
+}
+
+}  // namespace moe
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+namespace moe {
+
+hipError_t launch_gemm1_stream(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
+                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
+                               uint16_t* c_act, int max_active, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm1_stream_kernel, dim3(I / 16, max_active), dim3(64 * S1_SPLITK), 0, stream, hidden,
+                     hscale, T, w13, s13, hdr, perm_tok, c_act);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm2_stream(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
+                               const float* perm_w, float* partial, int max_active, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm2_stream_kernel, dim3(H / 16, max_active), dim3(64 * S2_SPLITK), 0, stream, c_act, w2,
+                     s2, hdr, perm_w, partial);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm1_tiled(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
+                              const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
+                              uint16_t* c_act, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm1_tiled_kernel, dim3(grid), dim3(256), 0, stream, hidden, hscale, T, w13, s13, hdr,
+                     perm_tok, c_act);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm2_tiled(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
+                              const float* perm_w, float* partial, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm2_tiled_kernel, dim3(grid), dim3(256), 0, stream, c_act, w2, s2, hdr, perm_w, partial);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const float* partial, const int32_t* tok_pair, int T, uint16_t* out, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, stream, partial, tok_pair, T, out);
+  return hipGetLastError();
+}
+
+}  // namespace moe

@@ -1,0 +1,195 @@
+"""Seeded synthetic inputs for the FP8 block-scale DeepSeek-V3 MoE operator.
+
+The operator's input schema (``reference moe/ref_moe.json:57-135``) fixes the
+shapes and dtypes; the distributions are the benchmark's:
+
+* ``routing_logits``  fp32 N(0, 1), [T, 256]
+* ``routing_bias``    bf16 N(0, 0.1), [256]
+* ``hidden_states``   N(0, 1) rounded to bf16, then OCP e4m3 with one fp32 scale
+  ``amax / 448`` per 1x128 block; scales stored transposed as [56, T]
+* ``gemm1_weights``   N(0, 0.02), [32, 4096, 7168], e4m3 with one fp32 scale
+  ``amax / 448`` per 128x128 block -> scales [32, 32, 56]
+* ``gemm2_weights``   N(0, 0.02), [32, 7168, 2048], e4m3 -> scales [32, 56, 16]
+
+Every tensor is a pure function of a numpy ``PCG64`` seed key (a tuple), so any
+one of them can be regenerated alone, on any host that has this numpy, and
+``fingerprint`` (sha256 over the raw bytes) checks that two hosts agree.
+The expert weights are shared by all workloads (one weight seed); each
+workload has its own activation seed.
+
+Skewed workload: ``local_expert_offset = 64`` makes global experts 64..95 (routing
+group 2) local. Four chosen local experts get +4.0 on their logits and every
+other expert of their routing group +2.0, so a few experts take most tokens.
+"""
+from __future__ import annotations
+
+import hashlib
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+H = 7168
+I = 2048
+E_GLOBAL = 256
+E_LOCAL = 32
+BLOCK = 128
+NB_H = H // BLOCK          # 56
+NB_I = I // BLOCK          # 16
+NB_G1 = 2 * I // BLOCK     # 32
+FP8_MAX = 448.0
+
+WEIGHT_SEED = 20261201
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    T: int
+    local_expert_offset: int
+    seed: int
+    skew: bool = False
+    routed_scaling_factor: float = 2.5
+
+
+# Activation seeds. T=1 and T=2 use the first seed (counting up from 1100 and
+# 1200) whose routing gives at least one local (token, expert) pair; the skewed
+# workload uses the first seed from 4000 whose selection margins (the gap between
+# the 4th and 5th group score and between the 8th and 9th candidate expert) are
+# at least 8 fp32 ulps on every token, so that selection cannot depend on the
+# last bit of exp().
+WORKLOADS = {
+    w.name: w
+    for w in [
+        Workload("t16", 16, 0, 1000),
+        Workload("decode_t1", 1, 0, 1102),
+        Workload("decode_t2", 2, 0, 1201),
+        Workload("decode_t4", 4, 0, 1300),
+        Workload("decode_t8", 8, 0, 1400),
+        Workload("decode_t32", 32, 0, 1500),
+        Workload("decode_t64", 64, 0, 1600),
+        Workload("prefill_t1024", 1024, 0, 2000),
+        Workload("prefill_t8192", 8192, 0, 3000),
+        Workload("skew_t4096", 4096, 64, 4002, skew=True),
+    ]
+}
+DECODE_SWEEP = ["decode_t1", "decode_t2", "decode_t4", "decode_t8", "decode_t32", "decode_t64"]
+
+SKEW_CHOSEN_LOCAL = (3, 11, 17, 29)
+
+
+def _rng(*key: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(list(key)))
+
+
+def _normal(key: tuple, shape, std: float) -> torch.Tensor:
+    x = _rng(*key).standard_normal(shape, dtype=np.float32)
+    t = torch.from_numpy(x)
+    if std != 1.0:
+        t.mul_(std)
+    return t
+
+
+def quantize_1x128(x: torch.Tensor):
+    """fp32 [T, H] -> (e4m3 [T, H], fp32 scale [H/128, T]) with scale = amax/448 per 1x128."""
+    T, h = x.shape
+    xb = x.view(T, h // BLOCK, BLOCK)
+    amax = xb.abs().amax(dim=2)
+    scale = torch.clamp(amax, min=1e-30) / FP8_MAX
+    q = (xb / scale.unsqueeze(2)).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.view(T, h), scale.t().contiguous()
+
+
+def quantize_128x128(w: torch.Tensor):
+    """fp32 [N, K] -> (e4m3 [N, K], fp32 scale [N/128, K/128]) with scale = amax/448 per block."""
+    n, k = w.shape
+    wb = w.view(n // BLOCK, BLOCK, k // BLOCK, BLOCK)
+    amax = wb.abs().amax(dim=(1, 3))
+    scale = torch.clamp(amax, min=1e-30) / FP8_MAX
+    q = (wb / scale[:, None, :, None]).clamp_(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.view(n, k), scale.contiguous()
+
+
+_WEIGHT_CACHE: dict = {}
+
+
+def make_weights(seed: int = WEIGHT_SEED, threads: int = 16):
+    """Expert weights (CPU tensors): (w13, s13, w2, s2) in the operator's layouts."""
+    if seed in _WEIGHT_CACHE:
+        return _WEIGHT_CACHE[seed]
+    w13 = torch.empty((E_LOCAL, 2 * I, H), dtype=torch.float8_e4m3fn)
+    s13 = torch.empty((E_LOCAL, NB_G1, NB_H), dtype=torch.float32)
+    w2 = torch.empty((E_LOCAL, H, I), dtype=torch.float8_e4m3fn)
+    s2 = torch.empty((E_LOCAL, NB_H, NB_I), dtype=torch.float32)
+
+    def one(job):
+        which, e = job
+        if which == 1:
+            q, s = quantize_128x128(_normal((seed, 1, e), (2 * I, H), 0.02))
+            w13[e].copy_(q)
+            s13[e].copy_(s)
+        else:
+            q, s = quantize_128x128(_normal((seed, 2, e), (H, I), 0.02))
+            w2[e].copy_(q)
+            s2[e].copy_(s)
+
+    jobs = [(1, e) for e in range(E_LOCAL)] + [(2, e) for e in range(E_LOCAL)]
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)  # parallelism comes from the job threads
+    try:
+        with ThreadPoolExecutor(max(1, threads)) as ex:
+            list(ex.map(one, jobs))
+    finally:
+        torch.set_num_threads(prev)
+    out = (w13, s13, w2, s2)
+    _WEIGHT_CACHE.clear()
+    _WEIGHT_CACHE[seed] = out
+    return out
+
+
+def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool = False):
+    """(routing_logits fp32 [T,256], routing_bias bf16 [256], hidden e4m3 [T,H], hidden_scale [56,T])."""
+    logits = _normal((seed, 10), (T, E_GLOBAL), 1.0)
+    if skew:
+        chosen = torch.tensor([local_expert_offset + c for c in SKEW_CHOSEN_LOCAL])
+        for g in sorted({int(c) // 32 for c in chosen}):
+            logits[:, g * 32:(g + 1) * 32] += 2.0
+        logits[:, chosen] += 2.0
+    bias = _normal((seed, 11), (E_GLOBAL,), 0.1).to(torch.bfloat16)
+    x = _normal((seed, 12), (T, H), 1.0).to(torch.bfloat16).to(torch.float32)
+    hidden, hidden_scale = quantize_1x128(x) if T > 0 else (
+        torch.empty((0, H), dtype=torch.float8_e4m3fn), torch.empty((NB_H, 0), dtype=torch.float32))
+    return logits, bias, hidden, hidden_scale
+
+
+def make_inputs(name_or_workload, device="cpu"):
+    """All ten operator inputs, in the reference's positional order, as a list."""
+    w = WORKLOADS[name_or_workload] if isinstance(name_or_workload, str) else name_or_workload
+    logits, bias, hidden, hidden_scale = make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    w13, s13, w2, s2 = make_weights()
+    args = [logits, bias, hidden, hidden_scale, w13, s13, w2, s2]
+    if device != "cpu":
+        args = [a.to(device) for a in args]
+    return args + [w.local_expert_offset, w.routed_scaling_factor]
+
+
+def fingerprint(t: torch.Tensor) -> str:
+    """sha256 of a tensor's raw bytes (contiguous, on the host)."""
+    t = t.detach().contiguous().cpu().reshape(-1)
+    if t.numel() == 0:
+        return hashlib.sha256(b"").hexdigest()
+    return hashlib.sha256(t.view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+def algorithmic_counts(P: int, E_act: int, T: int):
+    """(FLOPs, bytes) that one call must do at minimum.
+
+    FLOPs: 2*4096*7168 (GEMM1) + 2*2048*7168 (GEMM2) per routed (token, local expert) pair.
+    Bytes: per activated expert its fp8 W13 + W2 and their scales; per token the fp8 row,
+    its 56 scales, its 256 fp32 logits and its bf16 output row; plus the bf16 bias.
+    """
+    flops = P * (2 * 2 * I * H + 2 * I * H)
+    per_expert = 2 * I * H + H * I + (NB_G1 * NB_H + NB_H * NB_I) * 4
+    per_token = H + NB_H * 4 + E_GLOBAL * 4 + H * 2
+    return flops, E_act * per_expert + T * per_token + E_GLOBAL * 2

@@ -1,0 +1,106 @@
+/*
+ * C ABI of libmoe_mi355x.so: the FP8 block-scale DeepSeek-V3 MoE operator
+ * "moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048" for one GPU's
+ * 32-local-expert share, built for MI355X (gfx950).
+ *
+ * All tensor arguments are device pointers to row-major contiguous buffers,
+ * 16-byte aligned. Nothing here allocates, synchronises the host or throws:
+ * work is enqueued on `stream` (a hipStream_t, NULL = default stream) and
+ * errors come back as negative return codes (see moe_fp8_strerror).
+ * Calls on different streams are independent when each passes its own
+ * workspace; the only process-global state is a per-device cache of the
+ * compute-unit count and the path override below.
+ */
+#ifndef MOE_FP8_H
+#define MOE_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MOE_OK = 0,
+  MOE_ERR_NULL = -1,      /* a required pointer is NULL */
+  MOE_ERR_SIZE = -2,      /* T < 0 or T beyond MOE_FP8_MAX_TOKENS */
+  MOE_ERR_ALIGN = -3,     /* a pointer is not 16-byte aligned */
+  MOE_ERR_WORKSPACE = -4, /* workspace_bytes < moe_fp8_workspace_size(T) */
+  MOE_ERR_HIP = -5        /* a HIP launch failed; see moe_fp8_last_hip_error() */
+};
+
+#define MOE_FP8_MAX_TOKENS (1 << 20)
+
+/* Bytes of device workspace one forward call needs for T tokens (worst case
+ * of 8 routed local pairs per token). */
+size_t moe_fp8_workspace_size(int64_t T);
+
+/*
+ * Whole operator, destination-passing style.
+ * Replaces the reference's C++ entry point
+ *   void kernel(at::Tensor routing_logits, at::Tensor routing_bias,
+ *               at::Tensor hidden_states, at::Tensor hidden_states_scale,
+ *               at::Tensor gemm1_weights, at::Tensor gemm1_weights_scale,
+ *               at::Tensor gemm2_weights, at::Tensor gemm2_weights_scale,
+ *               int64_t local_expert_offset, double routed_scaling_factor,
+ *               at::Tensor output)                 (solution/cuda/kernel_v2.cu:146-158)
+ * and the Python `kernel(..., output)` of solution/triton/kernel.py:292-305,
+ * with the reference semantics of reference moe/ref_moe.py:4-168.
+ *
+ *   routing_logits       fp32 [T, 256]
+ *   routing_bias         bf16 [256] (raw bits)
+ *   hidden_states        e4m3 [T, 7168] (raw bytes)
+ *   hidden_states_scale  fp32 [56, T]   (one scale per 1x128 block, transposed)
+ *   gemm1_weights        e4m3 [32, 4096, 7168]; gemm1_weights_scale fp32 [32, 32, 56]
+ *   gemm2_weights        e4m3 [32, 7168, 2048]; gemm2_weights_scale fp32 [32, 56, 16]
+ *   output               bf16 [T, 7168] (raw bits), written in full
+ * Local experts are global ids [local_expert_offset, local_expert_offset + 32)
+ * clipped to [0, 256); tokens with no local expert get zeros.
+ */
+int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                    const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                    const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                    const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                    double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * Routing stage alone (reference moe/ref_moe.py:94-126; the sigmoid/bias kernel
+ * and top-k chain of solution/cuda/kernel_v2.cu:170-206).
+ * Writes, per token, the 8 selected global expert ids in ascending order
+ * (int32 [T, 8]) and their routing weights (fp32 [T, 8]). If tok_pair is not
+ * NULL every one of its T*8 slots is set to -1.
+ */
+int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
+                  double routed_scaling_factor, int32_t* topk_ids, float* topk_w, int32_t* tok_pair,
+                  void* stream);
+
+/*
+ * Dispatch stage alone (reference moe/ref_moe.py:131-145; the nonzero / sort /
+ * cumsum dispatch of solution/cuda/kernel_v2.cu:208-244, without its host sync).
+ * From the routing stage's ids and weights, writes
+ *   header   int32 [128]: counts[32], seg_start[33] (seg_start[32] = P),
+ *            n_active, active[32] (local ids with tokens, ascending), padding
+ *   perm_tok int32 [8T]: for each local expert in order, its tokens ascending
+ *   perm_w   fp32  [8T]: the routing weight of each (token, expert) pair
+ *   tok_pair int32 [T, 8]: pair index of slot j of token t; must hold -1 on
+ *            entry (moe_fp8_route sets that), local slots are overwritten.
+ */
+int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, int64_t local_expert_offset,
+                     int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair, void* stream);
+
+/* Expert-GEMM shape used by moe_fp8_forward: 0 = by token count (default),
+ * 1 = always the decode (stream) shape, 2 = always the prefill (tiled) shape.
+ * Process-global; meant for tests. Returns the previous value. */
+int moe_fp8_set_path(int path);
+
+const char* moe_fp8_strerror(int code);
+const char* moe_fp8_last_hip_error(void);
+int moe_fp8_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_FP8_H */

@@ -1,0 +1,203 @@
+"""Parity of the HIP operator with the reference (golden vectors) and the CPU oracle.
+
+Bars: expert selection and the per-expert permutation bit-exact; the bf16 output
+within atol=1e-2, rtol=2e-2 (torch.allclose semantics) of the reference.
+Everything goes through libmoe_mi355x.so's C ABI via flashinfer_mlsys_amd.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import flashinfer_mlsys_amd as fm
+from flashinfer_mlsys_amd import workloads as wl
+from oracle import cpu_ref
+
+from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden
+
+pytestmark = pytest.mark.gpu
+
+ALL = list(wl.WORKLOADS)
+SMALL = [n for n in ALL if wl.WORKLOADS[n].T <= 1024]
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="session")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def weights(dev):
+    _say("generating expert weights")
+    cpu = wl.make_weights()
+    with open(os.path.join(GOLDEN_DIR, "weights.json")) as f:
+        meta = json.load(f)
+    for t, k in zip(cpu, ["gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]):
+        assert wl.fingerprint(t) == meta[k], f"{k} does not regenerate identically on this host"
+    gpu = [t.to(dev) for t in cpu]
+    torch.cuda.synchronize()
+    return cpu, gpu
+
+
+class Case:
+    def __init__(self, name, weights, dev):
+        self.name = name
+        self.w = wl.WORKLOADS[name]
+        self.g = load_golden(name)
+        acts = wl.make_activations(self.w.T, self.w.seed, self.w.local_expert_offset, self.w.skew)
+        for a, h in zip(acts, self.g["in_sha256"]):
+            assert wl.fingerprint(a) == str(h), f"{name}: inputs do not regenerate identically"
+        self.cpu = list(acts) + list(weights[0])
+        self.gpu = [a.to(dev) for a in acts] + list(weights[1])
+        self.offset = self.w.local_expert_offset
+        self.rsf = self.w.routed_scaling_factor
+
+    def forward(self, offset=None):
+        return fm.run(*self.gpu, self.offset if offset is None else offset, self.rsf)
+
+
+_cases = {}
+
+
+@pytest.fixture
+def case(request, weights, dev):
+    name = request.param
+    if name not in _cases:
+        _say(f"case {name}")
+        _cases.clear()
+        _cases[name] = Case(name, weights, dev)
+    return _cases[name]
+
+
+@pytest.mark.parametrize("case", ALL, indirect=True)
+def test_route_selection_bit_exact(case):
+    ids, w, _ = fm.route(case.gpu[0], case.gpu[1], case.rsf)
+    ids = ids.cpu().numpy()
+    assert (np.diff(ids, axis=1) > 0).all(), "ids must be ascending and distinct per token"
+    np.testing.assert_array_equal(ids, case.g["sel_ids"].astype(np.int32))
+    # weights: the oracle's dense weights at the selected ids, to a few fp32 ulps
+    _, dense, _, _, _ = cpu_ref.route(case.cpu[0], case.cpu[1], case.rsf)
+    ref_w = torch.gather(dense, 1, torch.from_numpy(ids).long()).numpy()
+    np.testing.assert_allclose(w.cpu().numpy(), ref_w, rtol=4e-7 * 8, atol=0)
+
+
+@pytest.mark.parametrize("case", ALL, indirect=True)
+def test_dispatch_bit_exact(case):
+    ids, w, pair = fm.route(case.gpu[0], case.gpu[1], case.rsf)
+    header, perm_tok, perm_w, pair = fm.dispatch(ids, w, pair, case.offset)
+    h = header.cpu().numpy()
+    counts, seg = h[:32], h[32:65]
+    np.testing.assert_array_equal(counts, case.g["counts"])
+    assert seg[0] == 0 and (np.diff(seg) == counts).all()
+    P = int(seg[32])
+    np.testing.assert_array_equal(perm_tok.cpu().numpy()[:P], case.g["token_lists"])
+    n_act = h[65]
+    np.testing.assert_array_equal(h[66:66 + n_act], np.nonzero(counts)[0])
+    # perm_w is the routing weight of each pair; tok_pair points back at it
+    ids_c, w_c, pair_c = ids.cpu().numpy(), w.cpu().numpy(), pair.cpu().numpy()
+    pt, pw = perm_tok.cpu().numpy()[:P], perm_w.cpu().numpy()[:P]
+    local = (ids_c >= case.offset) & (ids_c < case.offset + 32)
+    assert ((pair_c >= 0) == local).all()
+    t_idx, j_idx = np.nonzero(local)
+    p_idx = pair_c[t_idx, j_idx]
+    assert sorted(p_idx.tolist()) == list(range(P))
+    np.testing.assert_array_equal(pt[p_idx], t_idx)
+    np.testing.assert_array_equal(pw[p_idx], w_c[t_idx, j_idx])
+
+
+@pytest.mark.parametrize("case", ALL, indirect=True)
+def test_forward_matches_reference(case):
+    out = case.forward()
+    torch.cuda.synchronize()
+    out_np = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    rows = case.g["out_rows"]
+    assert_close_bf16(bf16_bits_to_f32(out_np[rows]), bf16_bits_to_f32(case.g["out_bf16"]),
+                      f"{case.name} vs reference rows")
+    if case.w.T <= 1024:
+        ref = cpu_ref.run(*case.cpu, case.offset, case.rsf).float().numpy()
+        assert_close_bf16(bf16_bits_to_f32(out_np), ref, f"{case.name} vs oracle")
+    # tokens without a local expert are exact zeros
+    lists = golden_lists(case.g)
+    has = np.zeros(case.w.T, dtype=bool)
+    for l in lists:
+        has[l] = True
+    assert (out_np[~has] == 0).all()
+
+
+@pytest.mark.parametrize("case", ["t16", "decode_t64", "prefill_t1024"], indirect=True)
+def test_decode_and_prefill_shapes_agree(case):
+    old = fm.set_path(1)
+    try:
+        a = case.forward().float()
+        fm.set_path(2)
+        b = case.forward().float()
+    finally:
+        fm.set_path(old)
+    ref = bf16_bits_to_f32(case.g["out_bf16"])
+    rows = case.g["out_rows"]
+    assert_close_bf16(a.cpu().numpy()[rows], ref, "decode shape")
+    assert_close_bf16(b.cpu().numpy()[rows], ref, "prefill shape")
+    # both shapes compute the same sums in different order: they agree far inside the bar
+    d = (a - b).abs().max().item()
+    assert d <= 2e-2, d
+
+
+@pytest.mark.parametrize("case", ["decode_t8", "prefill_t1024", "skew_t4096"], indirect=True)
+def test_deterministic(case):
+    a = case.forward()
+    b = case.forward()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("case", ["prefill_t8192"], indirect=True)
+def test_token_permutation_equivariance(case):
+    """Each token's output depends only on its own row: permuting tokens permutes rows, bit for bit."""
+    T = case.w.T
+    perm = torch.from_numpy(np.random.default_rng(5).permutation(T)).to(case.gpu[0].device)
+    lg, b, h, hs = case.gpu[:4]
+    out = case.forward()
+    out_p = fm.run(lg[perm].contiguous(), b, h[perm].contiguous(), hs[:, perm].contiguous(), *case.gpu[4:],
+                   case.offset, case.rsf)
+    assert torch.equal(out_p.view(torch.int16), out[perm].view(torch.int16))
+
+
+@pytest.mark.parametrize("case", ["t16"], indirect=True)
+@pytest.mark.parametrize("offset", [256, -32, 1000, -1000])
+def test_no_local_expert_gives_zeros(case, offset):
+    out = case.forward(offset)
+    assert (out.view(torch.int16) == 0).all()
+
+
+@pytest.mark.parametrize("case", ["t16"], indirect=True)
+@pytest.mark.parametrize("offset", [224, 240, -16, 32])
+def test_other_offsets_match_oracle(case, offset):
+    """Offsets whose 32-expert window is partly outside [0, 256) skip those experts (ref_moe.py:134-137)."""
+    out = case.forward(offset).float().cpu().numpy()
+    ref = cpu_ref.run(*case.cpu, offset, case.rsf).float().numpy()
+    assert_close_bf16(out, ref, f"offset {offset}")
+
+
+def test_zero_tokens(weights, dev):
+    w13, s13, w2, s2 = weights[1]
+    lg = torch.empty((0, 256), dtype=torch.float32, device=dev)
+    b = torch.zeros(256, dtype=torch.bfloat16, device=dev)
+    h = torch.empty((0, 7168), dtype=torch.float8_e4m3fn, device=dev)
+    hs = torch.empty((56, 0), dtype=torch.float32, device=dev)
+    out = fm.run(lg, b, h, hs, w13, s13, w2, s2, 0, 2.5)
+    assert out.shape == (0, 7168)
+
+
+@pytest.mark.parametrize("case", ["t16"], indirect=True)
+def test_dps_writes_into_output(case):
+    out = torch.full((case.w.T, 7168), 7.0, dtype=torch.bfloat16, device=case.gpu[0].device)
+    ret = fm.kernel(*case.gpu, case.offset, case.rsf, out)
+    assert ret is None
+    ref = bf16_bits_to_f32(case.g["out_bf16"])
+    assert_close_bf16(out.float().cpu().numpy()[case.g["out_rows"]], ref, "dps")

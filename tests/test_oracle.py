@@ -1,0 +1,163 @@
+"""Pins the CPU oracle (no GPU): against the reference's own golden vectors,
+the OCP e4m3 spec, a brute-force routing search and a float64 recomputation;
+planted mistakes in the oracle must be caught by those same checks."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from flashinfer_mlsys_amd import workloads as wl
+from oracle import cpu_ref, np_ref
+
+from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden
+
+ALL = list(wl.WORKLOADS)
+
+
+def test_e4m3_decode_matches_spec():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    got = codes.view(torch.float8_e4m3fn).to(torch.float32).numpy().astype(np.float64)
+    want = np_ref.e4m3_table()
+    nan = np.isnan(want)
+    assert nan.sum() == 2 and np.isnan(got[nan]).all()
+    np.testing.assert_array_equal(got[~nan], want[~nan])
+    # spot values from the OCP table: max normal, min normal, min subnormal
+    assert np_ref.e4m3_value(0x7E) == 448.0
+    assert np_ref.e4m3_value(0x08) == 2.0 ** -6
+    assert np_ref.e4m3_value(0x01) == 2.0 ** -9
+
+
+@pytest.mark.parametrize("name", ALL)
+def test_inputs_regenerate(name):
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    assert [wl.fingerprint(a) for a in acts] == [str(h) for h in g["in_sha256"]]
+
+
+def test_weights_regenerate():
+    with open(os.path.join(GOLDEN_DIR, "weights.json")) as f:
+        meta = json.load(f)
+    ts = wl.make_weights()
+    for t, k in zip(ts, ["gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]):
+        assert wl.fingerprint(t) == meta[k], k
+
+
+@pytest.mark.parametrize("name", ALL)
+def test_oracle_routing_matches_reference(name):
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    topk_idx = cpu_ref.route(lg, b, w.routed_scaling_factor)[0]
+    np.testing.assert_array_equal(cpu_ref.sorted_selection(topk_idx).numpy(), g["sel_ids"].astype(np.int64))
+    lists = cpu_ref.dispatch(topk_idx, w.local_expert_offset)
+    np.testing.assert_array_equal([len(l) for l in lists], g["counts"])
+    for a, b_ in zip(lists, golden_lists(g)):
+        np.testing.assert_array_equal(a.numpy(), b_)
+
+
+@pytest.mark.parametrize("name", ["t16", "skew_t4096", "prefill_t1024"])
+def test_routing_brute_force(name):
+    """Exhaustive group-subset search (70 subsets) + full sort on the first 24 tokens."""
+    w = wl.WORKLOADS[name]
+    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    lg = lg[:24]
+    ids, wts = np_ref.brute_force_route(lg.numpy(), b.float().numpy(), w.routed_scaling_factor)
+    topk_idx, dense, _, _, _ = cpu_ref.route(lg, b, w.routed_scaling_factor)
+    sel = cpu_ref.sorted_selection(topk_idx).numpy()
+    np.testing.assert_array_equal(sel, ids)
+    np.testing.assert_allclose(np.take_along_axis(dense.numpy(), sel, 1), wts, rtol=1e-6)
+    # weights sum to rsf * S / (S + 1e-20) = rsf
+    np.testing.assert_allclose(dense.sum(1).numpy(), w.routed_scaling_factor, rtol=1e-6)
+
+
+def test_routing_invariants_t8192():
+    w = wl.WORKLOADS["prefill_t8192"]
+    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    topk_idx, dense, s, sb, gs = cpu_ref.route(lg, b, w.routed_scaling_factor)
+    sel = cpu_ref.sorted_selection(topk_idx)
+    assert (sel[:, 1:] > sel[:, :-1]).all()
+    groups = sel // 32
+    top4 = torch.topk(gs, 4, dim=1).indices
+    kept = torch.zeros_like(gs, dtype=torch.bool).scatter_(1, top4, True)
+    assert torch.gather(kept, 1, groups).all(), "every selected expert lies in a kept group"
+    # the selected set is the top-8 of the biased scores among the kept groups
+    cand = sb.masked_fill(~kept.repeat_interleave(32, 1), float("-inf"))
+    kth = torch.sort(cand, 1, descending=True).values[:, 7:8]
+    assert (torch.gather(sb, 1, sel) >= kth).all()
+    # unbiased weights: proportional to s over the selected set
+    ws = torch.gather(dense, 1, sel)
+    ratio = ws / torch.gather(s, 1, sel)
+    assert torch.allclose(ratio, ratio[:, :1].expand_as(ratio), rtol=1e-6)
+
+
+@pytest.mark.parametrize("name", ["t16", "decode_t1", "decode_t2", "decode_t8", "decode_t64"])
+def test_oracle_output_matches_reference(name):
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    args = wl.make_inputs(name)
+    out = cpu_ref.run(*args)
+    got = out.view(torch.int16).numpy().view(np.uint16)[g["out_rows"]]
+    assert_close_bf16(bf16_bits_to_f32(got), bf16_bits_to_f32(g["out_bf16"]), name)
+    # same torch build and thread count as the fixture: expect the reference's bits
+    if (str(g["torch_version"]) == torch.__version__ and int(g["num_threads"]) == torch.get_num_threads()
+            and str(g["cpu_capability"]) == torch.backends.cpu.get_cpu_capability()):
+        np.testing.assert_array_equal(got, g["out_bf16"])
+
+
+def test_oracle_rows_match_float64():
+    name = "t16"
+    w = wl.WORKLOADS[name]
+    args = wl.make_inputs(name)
+    out = cpu_ref.run(*args).float().numpy()
+    topk_idx, dense, _, _, _ = cpu_ref.route(args[0], args[1], w.routed_scaling_factor)
+    sel = cpu_ref.sorted_selection(topk_idx).numpy()
+    sel_w = np.take_along_axis(dense.numpy(), sel, 1)
+    tokens = [t for t in range(w.T) if ((sel >= 0) & (sel < 32)).any(1)[t]][:3]
+    u8 = lambda t: t.view(torch.uint8).numpy()
+    ref = np_ref.rows_fp64(tokens, sel, sel_w, u8(args[2]), args[3].numpy(), u8(args[4]), args[5].numpy(),
+                           u8(args[6]), args[7].numpy(), w.local_expert_offset)
+    np.testing.assert_allclose(out[tokens], ref, rtol=8e-3, atol=1e-4)
+
+
+# --- planted mistakes: each must make the checks above fail -----------------
+
+def _swapped_swiglu(A_e, W13_e, W2_e):
+    G1 = A_e.matmul(W13_e.t())
+    X1, X2 = G1[:, :cpu_ref.I], G1[:, cpu_ref.I:]
+    return ((X1 / (1.0 + torch.exp(-X1))) * X2).matmul(W2_e.t())
+
+
+def _transposed_block_scale(w, s):
+    wf = w.to(torch.float32)
+    sf = s.to(torch.float32)
+    d = wf.dim() - 2
+    sf = sf.transpose(d, d + 1).contiguous().reshape(sf.shape)  # scale blocks read in the wrong order
+    sf = torch.repeat_interleave(torch.repeat_interleave(sf, 128, dim=d), 128, dim=d + 1)
+    return wf * sf
+
+
+def _route_without_bias(logits, bias, rsf):
+    return _orig_route(logits, torch.zeros_like(bias), rsf)
+
+
+_orig_route = cpu_ref.route
+
+
+@pytest.mark.parametrize("mutation", ["swiglu_halves", "block_scale_order", "bias_dropped"])
+def test_planted_mistakes_are_caught(monkeypatch, mutation):
+    name = "t16"
+    g = load_golden(name)
+    args = wl.make_inputs(name)
+    if mutation == "swiglu_halves":
+        monkeypatch.setattr(cpu_ref, "expert_ffn", _swapped_swiglu)
+    elif mutation == "block_scale_order":
+        monkeypatch.setattr(cpu_ref, "dequant_weight", _transposed_block_scale)
+    else:
+        monkeypatch.setattr(cpu_ref, "route", _route_without_bias)
+    out = cpu_ref.run(*args)
+    got = bf16_bits_to_f32(out.view(torch.int16).numpy().view(np.uint16)[g["out_rows"]])
+    with pytest.raises(AssertionError):
+        assert_close_bf16(got, bf16_bits_to_f32(g["out_bf16"]), mutation)
