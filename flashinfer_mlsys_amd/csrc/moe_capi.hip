@@ -59,12 +59,17 @@ size_t moe_fp8_workspace_size(int64_t T) {
   return moe::WorkspaceLayout::make(T).total;
 }
 
-int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
-                    const float* hidden_states_scale, const uint8_t* gemm1_weights,
-                    const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
-                    const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
-                    double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Records events[i] (when given) before stage i and events[5] after the last:
+// route, dispatch, GEMM1+SwiGLU, GEMM2 x weight, combine.
+int forward_impl(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                 const float* hidden_states_scale, const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
+                 const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T,
+                 int64_t local_expert_offset, double routed_scaling_factor, uint16_t* output, void* workspace,
+                 size_t workspace_bytes, void* stream, void* const* events) {
   using namespace moe;
   if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
@@ -93,10 +98,16 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
   auto* partial = reinterpret_cast<float*>(ws + L.partial);
 
   hipError_t e;
+  auto mark = [&](int i) -> hipError_t {
+    return events ? hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), s) : hipSuccess;
+  };
+  if ((e = mark(0)) != hipSuccess) return hip_fail(e);
   if ((e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, tok_pair, s)) != hipSuccess)
     return hip_fail(e);
+  if ((e = mark(1)) != hipSuccess) return hip_fail(e);
   if ((e = launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)) != hipSuccess)
     return hip_fail(e);
+  if ((e = mark(2)) != hipSuccess) return hip_fail(e);
 
   const int path = g_path.load(std::memory_order_relaxed);
   const bool stream_shape = path == 1 || (path == 0 && t <= kStreamMaxTokens);
@@ -105,6 +116,7 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
     if ((e = launch_gemm1_stream(hidden_states, hidden_states_scale, t, gemm1_weights, gemm1_weights_scale, hdr,
                                  perm_tok, c_act, max_active, s)) != hipSuccess)
       return hip_fail(e);
+    if ((e = mark(3)) != hipSuccess) return hip_fail(e);
     if ((e = launch_gemm2_stream(c_act, gemm2_weights, gemm2_weights_scale, hdr, perm_w, partial, max_active, s)) !=
         hipSuccess)
       return hip_fail(e);
@@ -113,12 +125,44 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
     if ((e = launch_gemm1_tiled(hidden_states, hidden_states_scale, t, gemm1_weights, gemm1_weights_scale, hdr,
                                 perm_tok, c_act, grid, s)) != hipSuccess)
       return hip_fail(e);
+    if ((e = mark(3)) != hipSuccess) return hip_fail(e);
     if ((e = launch_gemm2_tiled(c_act, gemm2_weights, gemm2_weights_scale, hdr, perm_w, partial, grid, s)) !=
         hipSuccess)
       return hip_fail(e);
   }
+  if ((e = mark(4)) != hipSuccess) return hip_fail(e);
   if ((e = launch_combine(partial, tok_pair, t, output, s)) != hipSuccess) return hip_fail(e);
+  if ((e = mark(5)) != hipSuccess) return hip_fail(e);
   return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                    const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                    const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                    const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                    double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return forward_impl(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                      gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                      routed_scaling_factor, output, workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_fp8_forward_timed(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                          const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                          const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                          const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                          double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                          void* stream, void* const* events) {
+  if (!events) return MOE_ERR_NULL;
+  for (int i = 0; i < 6; ++i)
+    if (!events[i]) return MOE_ERR_NULL;
+  return forward_impl(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                      gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                      routed_scaling_factor, output, workspace, workspace_bytes, stream, events);
 }
 
 int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int64_t T,

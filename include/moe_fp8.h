@@ -66,6 +66,20 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
                     void* stream);
 
 /*
+ * moe_fp8_forward plus six caller-created hipEvent_t handles recorded on
+ * `stream` around the stages: events[0] before routing, [1] before dispatch,
+ * [2] before GEMM1+SwiGLU, [3] before GEMM2, [4] before the combine, [5] after.
+ * No reference counterpart (the reference timed its stages with torch.profiler,
+ * scripts/ncu_profile.py:89-143); used by bench.py for per-kernel durations.
+ */
+int moe_fp8_forward_timed(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                          const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                          const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                          const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                          double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                          void* stream, void* const* events);
+
+/*
  * Routing stage alone (reference moe/ref_moe.py:94-126; the sigmoid/bias kernel
  * and top-k chain of solution/cuda/kernel_v2.cu:170-206).
  * Writes, per token, the 8 selected global expert ids in ascending order
