@@ -9,10 +9,11 @@ operator call at each T of the sweep, with every input resident in HBM.
 Printed JSON line (rank 0, one line):
   value         tokens/s over the sweep = steps * sum(T) / wall time of the timed steps
   ms_per_step   wall time of one sweep
-  per_T         us/call, tokens/s and op-level HBM fraction per T (warm and cold L2/MALL)
+  per_T         us/call (back-to-back calls), tokens/s, op-level HBM fraction, the cold
+                (MALL flushed) call time and each stage's kernel time per T
   roofline      the dominant kernel (GEMM1 weight streaming): algorithmic bytes per
-                launch / its mean duration from HIP events recorded between the
-                operator's kernels, against the 8 TB/s HBM peak
+                launch / its mean duration (many back-to-back launches of that stage
+                between two HIP events on the operator's stream), against 8 TB/s
   cpu_baseline  the CPU oracle (PyTorch restatement of the reference, all 32 experts
                 dequantised per call as the reference does) timed on this host
   also          the other benchmark configurations (prefill 1024 / 8192, skew 4096)
@@ -40,7 +41,7 @@ METRIC = "µs/call & tokens/s, FP8 MoE 32 local experts, T=1…8192; % MFMA/HBM 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0   # dense e4m3 MFMA
 BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
-STAGES = ["route", "dispatch", "gemm1_swiglu", "gemm2_weight", "combine"]
+STAGES = ["route_dispatch", "gemm1", "gemm2", "combine"]
 
 W13_BYTES = 2 * wl.I * wl.H + wl.NB_G1 * wl.NB_H * 4     # one expert's fp8 W13 + its scales
 W2_BYTES = wl.H * wl.I + wl.NB_H * wl.NB_I * 4
@@ -77,28 +78,61 @@ class Runner:
         self.lib = _lib.load()
         self.ws_bytes = int(self.lib.moe_fp8_workspace_size(max_T))
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
-        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
-        for e in self.events:  # create the underlying hipEvents
-            e.record()
-        self.ev_array = (ctypes.c_void_p * 6)(*[e.cuda_event for e in self.events])
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def _args(self, c: Case):
+        return ([t.data_ptr() for t in c.args] + [c.T, c.offset, c.rsf, c.out.data_ptr(), self.ws.data_ptr(),
+                                                  self.ws_bytes, torch.cuda.current_stream(self.dev).cuda_stream])
+
+    def call(self, c: Case):
+        _lib.check(self.lib.moe_fp8_forward(*self._args(c)), "moe_fp8_forward")
+
+    def stage(self, c: Case, s: int):
+        _lib.check(self.lib.moe_fp8_run_stage(s, *self._args(c)), "moe_fp8_run_stage")
+
+    def graph(self, fn, reps):
+        """A HIP graph holding `reps` back-to-back calls of fn (captured on torch's stream)."""
+        fn()
         torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        return g
 
-    def call(self, c: Case, timed=False):
-        a = c.args
-        ptrs = [t.data_ptr() for t in a]
-        stream = torch.cuda.current_stream(self.dev).cuda_stream
-        if timed:
-            code = self.lib.moe_fp8_forward_timed(*ptrs, c.T, c.offset, c.rsf, c.out.data_ptr(), self.ws.data_ptr(),
-                                                  self.ws_bytes, stream, self.ev_array)
-        else:
-            code = self.lib.moe_fp8_forward(*ptrs, c.T, c.offset, c.rsf, c.out.data_ptr(), self.ws.data_ptr(),
-                                            self.ws_bytes, stream)
-        _lib.check(code, "moe_fp8_forward")
+    def graph_us(self, g, reps):
+        """Mean GPU us per captured call: one replay between two HIP events."""
+        self.ev[0].record()
+        g.replay()
+        self.ev[1].record()
+        torch.cuda.synchronize()
+        return self.ev[0].elapsed_time(self.ev[1]) / reps * 1e3
 
-    def stage_times_ms(self):
-        """Durations of the 5 stages of the last timed call (call after synchronize)."""
-        ev = self.events
-        return [ev[i].elapsed_time(ev[i + 1]) for i in range(5)]
+    def stage_us(self, c: Case, reps: int):
+        """Mean duration of each stage's kernel(s): a graph of `reps` back-to-back launches of that stage."""
+        self.call(c)
+        out = []
+        for s in range(4):
+            g = self.graph(lambda: self.stage(c, s), reps)
+            out.append(self.graph_us(g, reps))
+            del g
+        self.call(c)  # leave the workspace and output consistent
+        torch.cuda.synchronize()
+        return out
+
+    def cold_us(self, c: Case, reps: int, flush):
+        """Median us of one call after writing a buffer larger than the 256 MB MALL."""
+        ts = []
+        for _ in range(reps):
+            flush.add_(1)
+            self.ev[0].record()
+            self.call(c)
+            self.ev[1].record()
+            torch.cuda.synchronize()
+            ts.append(self.ev[0].elapsed_time(self.ev[1]) * 1e3)
+        return statistics.median(ts)
 
 
 def check_against_golden(c: Case):
@@ -117,19 +151,12 @@ def check_against_golden(c: Case):
     return True
 
 
-def time_calls(runner, c: Case, reps, flush=None):
-    """Per-call wall (events 0..5) and stage durations, medians over reps."""
-    totals, stages = [], []
-    for _ in range(reps):
-        if flush is not None:
-            flush.add_(1)
-        runner.call(c, timed=True)
-        torch.cuda.synchronize()
-        st = runner.stage_times_ms()
-        stages.append(st)
-        totals.append(runner.events[0].elapsed_time(runner.events[5]))
-    med = [statistics.median(s[i] for s in stages) for i in range(5)]
-    return statistics.median(totals), med, stages
+def time_plain(runner, c: Case, reps):
+    """GPU us per call: a graph of `reps` back-to-back calls, replayed between two events."""
+    g = runner.graph(lambda: runner.call(c), reps)
+    us = runner.graph_us(g, reps)
+    del g
+    return us
 
 
 def cpu_baseline(sweep_names):
@@ -189,76 +216,99 @@ def main():
         runner.call(c)
         torch.cuda.synchronize()
         check_against_golden(c)
+        for stage in range(4):  # the per-stage path must reproduce the forward's output
+            runner.stage(c, stage)
+        torch.cuda.synchronize()
+        check_against_golden(c)
     log("outputs match the reference rows")
 
     # --- headline: K timed sweeps, wall clock bracketed by synchronize -------------
+    # One step = one call at each T of the sweep, replayed from a HIP graph (as a
+    # decode server replays its captured step), so host launch cost is not timed.
     sweep_cases = [cases[n] for n in sweep]
+    step_graph = runner.graph(lambda: [runner.call(c) for c in sweep_cases], 1)
     for _ in range(args.warmup):
-        for c in sweep_cases:
-            runner.call(c)
+        step_graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        for c in sweep_cases:
-            runner.call(c)
+        step_graph.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
     tokens_per_step = sum(c.T for c in sweep_cases)
     value = args.steps * tokens_per_step / elapsed
-    log(f"sweep: {ms_per_step * 1e3:.1f} us/step, {value:.0f} tokens/s")
+    for c in sweep_cases:  # the replayed graph computed the right thing
+        check_against_golden(c)
+    # eager (one ctypes call per T, host launch cost included) for reference
+    for _ in range(2):
+        for c in sweep_cases:
+            runner.call(c)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        for c in sweep_cases:
+            runner.call(c)
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t1) / args.steps * 1e3
+    log(f"sweep: {ms_per_step * 1e3:.1f} us/step graph, {eager_ms * 1e3:.1f} us/step eager, {value:.0f} tokens/s")
 
-    # --- per-T and per-kernel figures from events between the operator's kernels ---
+    # --- per-T and per-kernel figures ------------------------------------------------
+    # Stage durations: `reps` back-to-back launches of one stage between two HIP
+    # events on the operator's stream (moe_fp8_run_stage), so no per-event cost.
     flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)  # > 256 MB MALL
-    per_T, g1_bytes, g1_ms = [], [], []
+    per_T, g1_bytes, g1_us = [], [], []
     for c in sweep_cases:
-        warm, st, all_st = time_calls(runner, c, args.reps)
-        cold, st_cold, _ = time_calls(runner, c, max(5, args.reps // 3), flush=flush)
-        for s in all_st:
-            g1_bytes.append(c.gemm1_bytes)
-            g1_ms.append(s[2])
+        plain = time_plain(runner, c, args.reps)
+        st = runner.stage_us(c, args.reps)
+        cold = runner.cold_us(c, max(5, args.reps // 3), flush)
+        g1_bytes.append(c.gemm1_bytes)
+        g1_us.append(st[1])
         per_T.append({
             "T": c.T, "P": c.P, "E_act": c.E_act,
-            "us_per_call": round(warm * 1e3, 2), "tokens_per_s": round(c.T / (warm * 1e-3), 1),
-            "hbm_frac": round(c.bytes / (warm * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-            "cold_us_per_call": round(cold * 1e3, 2),
-            "cold_hbm_frac": round(c.bytes / (cold * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-            "stage_us": {k: round(v * 1e3, 2) for k, v in zip(STAGES, st)},
-            "cold_stage_us": {k: round(v * 1e3, 2) for k, v in zip(STAGES, st_cold)},
+            "us_per_call": round(plain, 2), "tokens_per_s": round(c.T / (plain * 1e-6), 1),
+            "hbm_frac": round(c.bytes / (plain * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+            "cold_us_per_call": round(cold, 2),
+            "cold_hbm_frac": round(c.bytes / (cold * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+            "stage_us": {k: round(v, 2) for k, v in zip(STAGES, st)},
+            "gemm1_hbm_frac": round(c.gemm1_bytes / (st[1] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+            "gemm2_hbm_frac": round(c.gemm2_bytes / (st[2] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
         })
+        log(f"T={c.T}: {plain:.1f} us/call, stages {[round(x, 1) for x in st]}")
     del flush
     mean_bytes = statistics.fmean(g1_bytes)
-    mean_ms = statistics.fmean(g1_ms)
-    achieved = mean_bytes / (mean_ms * 1e-3) / 1e9
+    mean_us = statistics.fmean(g1_us)
+    achieved = mean_bytes / (mean_us * 1e-6) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("gemm1_stream_decode_sweep_bytes_per_launch")
+            traffic = json.load(f).get("gemm1_decode_kernel", {}).get("hbm_bytes_per_launch")
     roofline = {
-        "kernel": "gemm1_stream_kernel (GEMM1 + SwiGLU, decode shape)",
+        "kernel": "gemm1_decode_kernel (dispatch + GEMM1 + SwiGLU, T<=64)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-        "algorithmic_bytes_per_launch": round(mean_bytes), "mean_launch_us": round(mean_ms * 1e3, 2),
-        "launches": len(g1_ms),
+        "algorithmic_bytes_per_launch": round(mean_bytes), "mean_launch_us": round(mean_us, 2),
+        "timing": f"{args.reps} back-to-back launches per T between two HIP events, sweep mean",
     }
 
     also = {}
     for n in extra:
         c = cases[n]
-        reps = max(5, args.reps // 3) if c.T >= 4096 else args.reps
-        warm, st, _ = time_calls(runner, c, reps)
-        t_s = warm * 1e-3
+        reps = 5 if c.T >= 4096 else args.reps // 2
+        plain = time_plain(runner, c, reps)
+        st = runner.stage_us(c, reps)
+        t_s = plain * 1e-6
         also[n] = {
-            "T": c.T, "P": c.P, "E_act": c.E_act, "us_per_call": round(warm * 1e3, 1),
+            "T": c.T, "P": c.P, "E_act": c.E_act, "us_per_call": round(plain, 1),
             "tokens_per_s": round(c.T / t_s, 1),
             "mfma_frac_fp8_peak": round(c.flops / t_s / (FP8_PEAK_TFLOPS * 1e12), 4),
             "hbm_frac": round(c.bytes / t_s / (HBM_PEAK_GBS * 1e9), 4),
-            "stage_us": {k: round(v * 1e3, 1) for k, v in zip(STAGES, st)},
-            "gemm1_tflops": round(c.P * GEMM1_FLOPS_PER_PAIR / (st[2] * 1e-3) / 1e12, 1),
-            "gemm2_tflops": round(c.P * GEMM2_FLOPS_PER_PAIR / (st[3] * 1e-3) / 1e12, 1),
+            "stage_us": {k: round(v, 1) for k, v in zip(STAGES, st)},
+            "gemm1_tflops": round(c.P * GEMM1_FLOPS_PER_PAIR / (st[1] * 1e-6) / 1e12, 1),
+            "gemm2_tflops": round(c.P * GEMM2_FLOPS_PER_PAIR / (st[2] * 1e-6) / 1e12, 1),
         }
-        log(f"{n}: {also[n]['us_per_call']} us/call")
+        log(f"{n}: {also[n]['us_per_call']} us/call, stages {[round(x, 1) for x in st]}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -283,6 +333,8 @@ def main():
             "workload": "decode sweep T=1,2,4,8,32,64: DeepSeek-V3 MoE shard, 32 local experts (offset 0) "
                         "of 256, hidden 7168, intermediate 2048, top-8, 8 groups / top-4, rsf 2.5",
             "tokens_per_step": tokens_per_step,
+            "launch": "one HIP graph replay per step (6 operator calls); eager ctypes calls: "
+                      f"{eager_ms:.4f} ms/step",
             "device": torch.cuda.get_device_name(dev),
         },
         "roofline": roofline,

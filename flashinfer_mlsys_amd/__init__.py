@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["kernel", "run", "route", "dispatch", "workspace_size", "MoEInputError", "set_path"]
+__all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "workspace_size", "MoEInputError", "set_path"]
 
 H = 7168
 I = 2048
@@ -190,3 +190,34 @@ def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
                                             tok_pair.data_ptr() if T else header.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_dispatch")
     return header, perm_tok, perm_w, tok_pair
+
+
+@torch.no_grad()
+def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor):
+    """Routing + dispatch exactly as ``kernel`` runs them.
+
+    Returns (topk_ids int32 [T, 8], topk_w fp32 [T, 8], header int32 [128],
+    perm_tok int32 [8T], perm_w fp32 [8T], tok_pair int32 [T, 8]).
+    """
+    _on_gpu(routing_logits, "routing_logits")
+    _req(routing_logits.dtype == torch.float32 and routing_logits.dim() == 2
+         and routing_logits.shape[1] == E_GLOBAL, "routing_logits must be float32 [T, 256]")
+    _req(routing_bias.dtype == torch.bfloat16 and routing_bias.numel() == E_GLOBAL, "routing_bias must be bf16 [256]")
+    T = routing_logits.shape[0]
+    dev = routing_logits.device
+    ids = torch.empty((T, TOP_K), dtype=torch.int32, device=dev)
+    w = torch.empty((T, TOP_K), dtype=torch.float32, device=dev)
+    header = torch.zeros(128, dtype=torch.int32, device=dev)
+    perm_tok = torch.full((max(1, TOP_K * T),), -1, dtype=torch.int32, device=dev)
+    perm_w = torch.zeros((max(1, TOP_K * T),), dtype=torch.float32, device=dev)
+    pair = torch.full((T, TOP_K), -7, dtype=torch.int32, device=dev)
+    if T == 0:
+        return ids, w, header, perm_tok, perm_w, pair
+    lg, b = _contig(routing_logits), _contig(routing_bias.reshape(-1))
+    with torch.cuda.device(dev):
+        code = _lib.load().moe_fp8_route_dispatch(lg.data_ptr(), b.data_ptr(), T, int(local_expert_offset),
+                                                  float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(),
+                                                  header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
+                                                  pair.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_route_dispatch")
+    return ids, w, header, perm_tok, perm_w, pair

@@ -25,10 +25,11 @@ SIGNATURES = {
     "moe_fp8_workspace_size": (ctypes.c_size_t, [_I64]),
     "moe_fp8_forward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double, _P, _P,
                                        ctypes.c_size_t, _P]),
-    "moe_fp8_forward_timed": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double, _P,
-                                             _P, ctypes.c_size_t, _P, _P]),
+    "moe_fp8_run_stage": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double,
+                                         _P, _P, ctypes.c_size_t, _P]),
     "moe_fp8_route": (ctypes.c_int, [_P, _P, _I64, ctypes.c_double, _P, _P, _P, _P]),
     "moe_fp8_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "moe_fp8_route_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P, _P, _P, _P, _P]),
     "moe_fp8_set_path": (ctypes.c_int, [ctypes.c_int]),
     "moe_fp8_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "moe_fp8_last_hip_error": (ctypes.c_char_p, []),

@@ -5,16 +5,21 @@
 #include "moe_common.h"
 #include "../../include/moe_fp8.h"
 
+#include <algorithm>
 #include <atomic>
 
 namespace moe {
 hipError_t launch_route(const float*, const uint16_t*, int, float, int32_t*, float*, int32_t*, hipStream_t);
 hipError_t launch_dispatch(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
                            hipStream_t);
-hipError_t launch_gemm1_stream(const uint8_t*, const float*, int, const uint8_t*, const float*,
-                               const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
-hipError_t launch_gemm2_stream(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
-                               float*, int, hipStream_t);
+hipError_t launch_dispatch_small(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
+                                 hipStream_t);
+hipError_t launch_gemm1_decode(const uint8_t*, const float*, int, int, const uint8_t*, const float*, const int32_t*,
+                               const float*, DispatchHeader*, int32_t*, float*, int32_t*, uint16_t*, int,
+                               hipStream_t);
+hipError_t launch_gemm2_combine_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*,
+                                       const float*, const int32_t*, int, uint16_t*, int, hipStream_t);
+int gemm1_decode_blocks_per_cu();
 hipError_t launch_gemm1_tiled(const uint8_t*, const float*, int, const uint8_t*, const float*,
                               const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_tiled(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
@@ -25,7 +30,7 @@ hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStrea
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kStreamMaxTokens = 64;  // decode shape up to this many tokens
+constexpr int kDecodeMaxTokens = 64;  // decode shape (LDS dispatch, streaming GEMMs) up to this many tokens
 std::atomic<int> g_cu_count[kMaxDevices];
 std::atomic<int> g_path{0};
 thread_local const char* t_last_hip_error = "no error";
@@ -63,13 +68,32 @@ size_t moe_fp8_workspace_size(int64_t T) {
 
 namespace {
 
-// Records events[i] (when given) before stage i and events[5] after the last:
-// route, dispatch, GEMM1+SwiGLU, GEMM2 x weight, combine.
-int forward_impl(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
-                 const float* hidden_states_scale, const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
-                 const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T,
-                 int64_t local_expert_offset, double routed_scaling_factor, uint16_t* output, void* workspace,
-                 size_t workspace_bytes, void* stream, void* const* events) {
+struct Call {
+  const float* logits;
+  const uint16_t* bias;
+  const uint8_t* hidden;
+  const float* hscale;
+  const uint8_t* w13;
+  const float* s13;
+  const uint8_t* w2;
+  const float* s2;
+  int T;
+  int offset;
+  float rsf;
+  uint16_t* out;
+  bool decode;  // T <= 64 and not forced to the prefill shape
+  hipStream_t stream;
+  moe::DispatchHeader* hdr;
+  int32_t *topk_ids, *tok_pair, *perm_tok;
+  float *topk_w, *perm_w, *partial;
+  uint16_t* c_act;
+};
+
+int check_call(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+               const float* hidden_states_scale, const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
+               const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+               double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes, void* stream,
+               Call& c) {
   using namespace moe;
   if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
@@ -82,58 +106,67 @@ int forward_impl(const float* routing_logits, const uint16_t* routing_bias, cons
     return MOE_ERR_ALIGN;
   const WorkspaceLayout L = WorkspaceLayout::make(T);
   if (workspace_bytes < L.total) return MOE_ERR_WORKSPACE;
-
-  const int t = (int)T;
-  const int off = clamp_offset(local_expert_offset);
-  const float rsf = (float)routed_scaling_factor;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  auto* hdr = reinterpret_cast<DispatchHeader*>(ws + L.hdr);
-  auto* topk_ids = reinterpret_cast<int32_t*>(ws + L.topk_ids);
-  auto* topk_w = reinterpret_cast<float*>(ws + L.topk_w);
-  auto* tok_pair = reinterpret_cast<int32_t*>(ws + L.tok_pair);
-  auto* perm_tok = reinterpret_cast<int32_t*>(ws + L.perm_tok);
-  auto* perm_w = reinterpret_cast<float*>(ws + L.perm_w);
-  auto* c_act = reinterpret_cast<uint16_t*>(ws + L.c_act);
-  auto* partial = reinterpret_cast<float*>(ws + L.partial);
+  c.logits = routing_logits;
+  c.bias = routing_bias;
+  c.hidden = hidden_states;
+  c.hscale = hidden_states_scale;
+  c.w13 = gemm1_weights;
+  c.s13 = gemm1_weights_scale;
+  c.w2 = gemm2_weights;
+  c.s2 = gemm2_weights_scale;
+  c.T = (int)T;
+  c.offset = clamp_offset(local_expert_offset);
+  c.rsf = (float)routed_scaling_factor;
+  c.out = output;
+  c.decode = g_path.load(std::memory_order_relaxed) != 2 && T <= kDecodeMaxTokens;
+  c.stream = reinterpret_cast<hipStream_t>(stream);
+  c.hdr = reinterpret_cast<DispatchHeader*>(ws + L.hdr);
+  c.topk_ids = reinterpret_cast<int32_t*>(ws + L.topk_ids);
+  c.topk_w = reinterpret_cast<float*>(ws + L.topk_w);
+  c.tok_pair = reinterpret_cast<int32_t*>(ws + L.tok_pair);
+  c.perm_tok = reinterpret_cast<int32_t*>(ws + L.perm_tok);
+  c.perm_w = reinterpret_cast<float*>(ws + L.perm_w);
+  c.c_act = reinterpret_cast<uint16_t*>(ws + L.c_act);
+  c.partial = reinterpret_cast<float*>(ws + L.partial);
+  return 1;  // valid, work to do
+}
 
-  hipError_t e;
-  auto mark = [&](int i) -> hipError_t {
-    return events ? hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), s) : hipSuccess;
-  };
-  if ((e = mark(0)) != hipSuccess) return hip_fail(e);
-  if ((e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, tok_pair, s)) != hipSuccess)
-    return hip_fail(e);
-  if ((e = mark(1)) != hipSuccess) return hip_fail(e);
-  if ((e = launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)) != hipSuccess)
-    return hip_fail(e);
-  if ((e = mark(2)) != hipSuccess) return hip_fail(e);
-
-  const int path = g_path.load(std::memory_order_relaxed);
-  const bool stream_shape = path == 1 || (path == 0 && t <= kStreamMaxTokens);
-  if (stream_shape) {
-    const int max_active = t * TOP_K < E_LOCAL ? t * TOP_K : E_LOCAL;
-    if ((e = launch_gemm1_stream(hidden_states, hidden_states_scale, t, gemm1_weights, gemm1_weights_scale, hdr,
-                                 perm_tok, c_act, max_active, s)) != hipSuccess)
-      return hip_fail(e);
-    if ((e = mark(3)) != hipSuccess) return hip_fail(e);
-    if ((e = launch_gemm2_stream(c_act, gemm2_weights, gemm2_weights_scale, hdr, perm_w, partial, max_active, s)) !=
-        hipSuccess)
-      return hip_fail(e);
-  } else {
-    const int grid = (cu_count() * 2 + 7) / 8 * 8;
-    if ((e = launch_gemm1_tiled(hidden_states, hidden_states_scale, t, gemm1_weights, gemm1_weights_scale, hdr,
-                                perm_tok, c_act, grid, s)) != hipSuccess)
-      return hip_fail(e);
-    if ((e = mark(3)) != hipSuccess) return hip_fail(e);
-    if ((e = launch_gemm2_tiled(c_act, gemm2_weights, gemm2_weights_scale, hdr, perm_w, partial, grid, s)) !=
-        hipSuccess)
-      return hip_fail(e);
+// Stage 0: routing (+ dispatch in the prefill shape); 1: GEMM1 + SwiGLU (+ the
+// in-workgroup dispatch in the decode shape); 2: GEMM2 x weight (+ the ordered
+// combine in the decode shape); 3: the combine (prefill shape only).
+hipError_t run_stage(int stage, const Call& c) {
+  using namespace moe;
+  const int max_active = c.T * TOP_K < E_LOCAL ? c.T * TOP_K : E_LOCAL;
+  switch (stage) {
+    case 0:
+      if (c.decode) return launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, nullptr, c.stream);
+      {
+        hipError_t e = launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, c.tok_pair, c.stream);
+        if (e != hipSuccess) return e;
+        return launch_dispatch(c.topk_ids, c.topk_w, c.T, c.offset, c.hdr, c.perm_tok, c.perm_w, c.tok_pair,
+                               c.stream);
+      }
+    case 1:
+      if (c.decode) {
+        const int grid = std::min(max_active * (I / 8), cu_count() * gemm1_decode_blocks_per_cu());
+        return launch_gemm1_decode(c.hidden, c.hscale, c.T, c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr,
+                                   c.perm_tok, c.perm_w, c.tok_pair, c.c_act, grid, c.stream);
+      }
+      return launch_gemm1_tiled(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
+                                (cu_count() * 2 + 7) / 8 * 8, c.stream);
+    case 2:
+      if (c.decode)
+        return launch_gemm2_combine_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.tok_pair, c.T, c.out, H / 16,
+                                           c.stream);
+      return launch_gemm2_tiled(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() * 2 + 7) / 8 * 8,
+                                c.stream);
+    case 3:
+      if (c.decode) return hipSuccess;
+      return launch_combine(c.partial, c.tok_pair, c.T, c.out, c.stream);
+    default:
+      return hipErrorInvalidValue;
   }
-  if ((e = mark(4)) != hipSuccess) return hip_fail(e);
-  if ((e = launch_combine(partial, tok_pair, t, output, s)) != hipSuccess) return hip_fail(e);
-  if ((e = mark(5)) != hipSuccess) return hip_fail(e);
-  return MOE_OK;
 }
 
 }  // namespace
@@ -146,23 +179,32 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
                     const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
                     double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
                     void* stream) {
-  return forward_impl(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
-                      gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
-                      routed_scaling_factor, output, workspace, workspace_bytes, stream, nullptr);
+  Call c;
+  const int v = check_call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                           routed_scaling_factor, output, workspace, workspace_bytes, stream, c);
+  if (v <= 0) return v;
+  for (int stage = 0; stage < 4; ++stage) {
+    const hipError_t e = run_stage(stage, c);
+    if (e != hipSuccess) return hip_fail(e);
+  }
+  return MOE_OK;
 }
 
-int moe_fp8_forward_timed(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
-                          const float* hidden_states_scale, const uint8_t* gemm1_weights,
-                          const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
-                          const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
-                          double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
-                          void* stream, void* const* events) {
-  if (!events) return MOE_ERR_NULL;
-  for (int i = 0; i < 6; ++i)
-    if (!events[i]) return MOE_ERR_NULL;
-  return forward_impl(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
-                      gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
-                      routed_scaling_factor, output, workspace, workspace_bytes, stream, events);
+int moe_fp8_run_stage(int stage, const float* routing_logits, const uint16_t* routing_bias,
+                      const uint8_t* hidden_states, const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                      const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                      const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                      double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  if (stage < 0 || stage > 3) return MOE_ERR_SIZE;
+  Call c;
+  const int v = check_call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                           routed_scaling_factor, output, workspace, workspace_bytes, stream, c);
+  if (v <= 0) return v;
+  const hipError_t e = run_stage(stage, c);
+  return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
 int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
@@ -189,6 +231,32 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
   hipError_t e = moe::launch_dispatch(topk_ids, topk_w, (int)T, clamp_offset(local_expert_offset),
                                       reinterpret_cast<moe::DispatchHeader*>(header), perm_tok, perm_w, tok_pair,
                                       reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MOE_OK : hip_fail(e);
+}
+
+int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
+                           int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
+                           float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
+                           void* stream) {
+  using namespace moe;
+  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T == 0) return MOE_OK;
+  if (!routing_logits || !routing_bias || !topk_ids || !topk_w || !header || !perm_tok || !perm_w || !tok_pair)
+    return MOE_ERR_NULL;
+  if (!aligned16(routing_logits) || !aligned16(routing_bias) || !aligned16(topk_ids) || !aligned16(topk_w) ||
+      !aligned16(header) || !aligned16(perm_tok) || !aligned16(perm_w) || !aligned16(tok_pair))
+    return MOE_ERR_ALIGN;
+  const int t = (int)T, off = clamp_offset(local_expert_offset);
+  const float rsf = (float)routed_scaling_factor;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto* hdr = reinterpret_cast<DispatchHeader*>(header);
+  hipError_t e;
+  const bool decode = g_path.load(std::memory_order_relaxed) != 2 && t <= kDecodeMaxTokens;
+  e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, decode ? nullptr : tok_pair, s);
+  if (e == hipSuccess) {
+    e = decode ? launch_dispatch_small(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)
+               : launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s);
+  }
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 

@@ -14,15 +14,16 @@
 // the bf16 C keeps the SwiGLU output to 8 significant bits.
 //
 // Two shapes of each GEMM:
-//   *_stream  -- few rows per expert (decode). One workgroup per (active expert,
-//                16-column tile); its waves split K and preload their whole weight
-//                slice into registers, so each weight byte is read once and all
-//                loads are in flight together. Partial sums meet in LDS.
+//   *_decode  -- few rows per expert. Persistent workgroups walk (active expert,
+//                column tile) items; the waves split K and preload their whole
+//                weight slice into registers, so each weight byte is read once
+//                and all loads are in flight together. Partial sums meet in LDS.
 //   *_tiled   -- many rows per expert (prefill). Persistent workgroups walk a
 //                device-built list of (expert, row tile, column tile) items with
 //                double-buffered LDS tiles; consecutive items share the weight
 //                tile and are kept on one XCD so its L2 serves the repeats.
 #include "moe_common.h"
+#include "moe_small_dispatch.h"
 
 namespace moe {
 
@@ -55,157 +56,231 @@ __device__ __forceinline__ float silu_mul(float x1, float x2) {
 __device__ __forceinline__ int xcd_remap(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
 
 // ---------------------------------------------------------------------------
-// GEMM1 + SwiGLU, stream shape
+// GEMM1 + SwiGLU, decode shape (T <= 64).
+//
+// Every workgroup first derives the dispatch from the routing output in its own
+// LDS (dispatch_small), so the weight stream starts without reading a header
+// back from memory; workgroup 0 also stores the dispatch for GEMM2.
+// Items are (active expert, 8-column tile): the MFMA's 16 B columns are W13
+// rows n..n+7 (X1) in lanes 0-7 and 2048+n..2048+n+7 (X2) in lanes 8-15, so
+// one expert spreads over 256 items and column c's X1 and X2 meet in the LDS
+// reduction. Each of the 8 waves owns 7 of the 56 K blocks. A workgroup (one
+// per CU) takes a contiguous run of items, so consecutive items mostly share
+// the expert: an expert with at most 16 rows keeps its activation fragments in
+// registers across items and only the weights stream, double-buffered in
+// registers (item i+1's weights are in flight while item i computes).
 // ---------------------------------------------------------------------------
-constexpr int S1_SPLITK = 8;                   // waves per workgroup, one K slice each
-constexpr int S1_KPW = NB_H / S1_SPLITK;       // 7 K blocks per wave
-constexpr int S1_MT = 2;                       // 16-row tiles per pass
-static_assert(NB_H % S1_SPLITK == 0, "K slices");
+constexpr int D1_WAVES = 8;
+constexpr int D1_KPW = NB_H / D1_WAVES;  // 7 K blocks per wave
+constexpr int D1_NT = I / 8;             // items per expert
+static_assert(NB_H % D1_WAVES == 0, "K slices");
+static_assert(64 * D1_WAVES >= SMALL_P, "dispatch_small needs 512 threads");
 
-__global__ __launch_bounds__(64 * S1_SPLITK) void gemm1_stream_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
-    const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
-  __shared__ float red[S1_SPLITK][S1_MT][2][4][64];
-  const int slot = blockIdx.y;
-  if (slot >= hdr->n_active) return;
-  const int le = hdr->active[slot];
-  const int cnt = hdr->counts[le], seg = hdr->seg_start[le];
-  const int nt = blockIdx.x;  // pair columns [16 nt, 16 nt + 16)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int col = lane & 15, kg = lane >> 4;
-  const int kb0 = wave * S1_KPW;
+struct G1Shared {
+  SmallDispatch d;
+  float red[D1_WAVES][4][64];
+  __attribute__((aligned(16))) float sa[NB_H][SMALL_T];  // activation scales of the current expert's rows
+};
 
-  const uint8_t* wu = w13 + ((size_t)le * N1 + nt * 16 + col) * H + kg * 32;
-  const uint8_t* wg = wu + (size_t)I * H;
-  const float* su = s13 + ((size_t)le * NB_N1 + (nt * 16) / BLK) * NB_H;
-  const float* sg = su + (size_t)NB_I * NB_H;
-  v8i bu[S1_KPW], bg[S1_KPW];
-#pragma unroll
-  for (int kk = 0; kk < S1_KPW; ++kk) {
-    bu[kk] = load_v8i(wu + (kb0 + kk) * BLK);
-    bg[kk] = load_v8i(wg + (kb0 + kk) * BLK);
-  }
+struct G1State {
+  int cur_le = -1;
+  bool a_resident = false;  // a[] holds rows 0..15 of expert cur_le
+};
 
-  for (int m0 = 0; m0 < cnt; m0 += 16 * S1_MT) {
-    int tok_a[S1_MT], tok_o[S1_MT][4];
+__device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __restrict__ w13, int le, int nt, int kb0) {
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int wrow = fr < 8 ? nt * 8 + fr : I + nt * 8 + (fr - 8);
+  const uint8_t* wp = w13 + ((size_t)le * N1 + wrow) * H + kb0 * BLK + kg * 32;
 #pragma unroll
-    for (int mt = 0; mt < S1_MT; ++mt) {
-      tok_a[mt] = perm_tok[seg + min(m0 + mt * 16 + col, cnt - 1)];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tok_o[mt][r] = perm_tok[seg + min(m0 + mt * 16 + 4 * kg + r, cnt - 1)];
-    }
-    v4f au[S1_MT], ag[S1_MT];
-#pragma unroll
-    for (int mt = 0; mt < S1_MT; ++mt) { au[mt] = v4f{0.f, 0.f, 0.f, 0.f}; ag[mt] = au[mt]; }
-#pragma unroll
-    for (int kk = 0; kk < S1_KPW; ++kk) {
-      const int kb = kb0 + kk;
-      const float swu = su[kb], swg = sg[kb];
-#pragma unroll
-      for (int mt = 0; mt < S1_MT; ++mt) {
-        const v8i a = load_v8i(hidden + (size_t)tok_a[mt] * H + kb * BLK + kg * 32);
-        const v4f pu = mfma_fp8_k128(a, bu[kk]);
-        const v4f pg = mfma_fp8_k128(a, bg[kk]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float sa = hscale[(size_t)kb * T + tok_o[mt][r]];
-          au[mt][r] += pu[r] * (sa * swu);
-          ag[mt][r] += pg[r] * (sa * swg);
-        }
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < S1_MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        red[wave][mt][0][r][lane] = au[mt][r];
-        red[wave][mt][1][r][lane] = ag[mt][r];
-      }
+  for (int kk = 0; kk < D1_KPW; ++kk) b[kk] = load_v8i(wp + kk * BLK);
+}
+
+// One item (expert, 8-column tile) with its weights already requested into b;
+// requests the next item's weights into bn once this item's activation loads
+// are out (so waiting for those never waits for the prefetch).
+__device__ __forceinline__ void g1_item(int item, int next, v8i (&a)[D1_KPW], v8i (&b)[D1_KPW], v8i (&bn)[D1_KPW],
+                                        G1State& st, G1Shared& sh, const uint8_t* __restrict__ hidden,
+                                        const float* __restrict__ hscale, int T, const uint8_t* __restrict__ w13,
+                                        const float* __restrict__ s13, uint16_t* __restrict__ c_act) {
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kb0 = wave * D1_KPW;
+  const SmallDispatch& d = sh.d;
+  const int le = __builtin_amdgcn_readfirstlane(d.active[item / D1_NT]), nt = item % D1_NT;
+  const int cnt = __builtin_amdgcn_readfirstlane(d.cnt[le]), seg = __builtin_amdgcn_readfirstlane(d.seg[le]);
+  if (le != st.cur_le) {  // uniform over the workgroup
     __syncthreads();
-    {
-      static_assert(S1_MT * 4 * 64 == 64 * S1_SPLITK, "one output per thread");
-      const int mt = tid >> 8, r = (tid >> 6) & 3, ln = tid & 63;
-      float x1 = 0.f, x2 = 0.f;
+    for (int i = tid; i < NB_H * cnt; i += blockDim.x) {
+      const int kb = i / cnt, r = i - kb * cnt;
+      sh.sa[kb][r] = hscale[(size_t)kb * T + d.tok[seg + r]];
+    }
+    __syncthreads();
+    st.cur_le = le;
+    st.a_resident = false;
+  }
+  // weight scales: the X1 block row (lanes 0-7) or the X2 block row (lanes 8-15), scalar loads
+  const float* su = s13 + ((size_t)le * NB_N1 + (nt * 8) / BLK) * NB_H + kb0;
+  const float* sg = su + (size_t)NB_I * NB_H;
+  bool prefetched = false;
+  for (int m0 = 0; m0 < cnt; m0 += 16) {
+    if (!st.a_resident) {
+      const int tok = d.tok[seg + min(m0 + fr, cnt - 1)];
+      const uint8_t* ap = hidden + (size_t)tok * H + kb0 * BLK + kg * 32;
 #pragma unroll
-      for (int w = 0; w < S1_SPLITK; ++w) {
-        x1 += red[w][mt][0][r][ln];
-        x2 += red[w][mt][1][r][ln];
+      for (int kk = 0; kk < D1_KPW; ++kk) a[kk] = load_v8i(ap + kk * BLK);
+      st.a_resident = cnt <= 16;
+    }
+    if (!prefetched) {
+      if (next >= 0) g1_load_w(bn, w13, __builtin_amdgcn_readfirstlane(d.active[next / D1_NT]), next % D1_NT, kb0);
+      prefetched = true;
+    }
+    if (m0 > 0) g1_load_w(b, w13, le, nt, kb0);  // later 16-row passes of a big expert re-read the tile
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < D1_KPW; ++kk) {
+      const v4f p = mfma_fp8_k128(a[kk], b[kk]);
+      const float sw = fr < 8 ? su[kk] : sg[kk];
+      const v4f sa = *reinterpret_cast<const v4f*>(&sh.sa[kb0 + kk][m0 + 4 * kg]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += p[r] * (sa[r] * sw);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh.red[wave][r][lane] = acc[r];
+    __syncthreads();
+    if (tid < 256) {
+      const int r = tid >> 6, ln = tid & 63;
+      if ((ln & 15) < 8) {
+        float x1 = 0.f, x2 = 0.f;
+#pragma unroll
+        for (int w = 0; w < D1_WAVES; ++w) {
+          x1 += sh.red[w][r][ln];
+          x2 += sh.red[w][r][ln + 8];
+        }
+        const int row = m0 + 4 * (ln >> 4) + r;
+        if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = f32_to_bf16_rne(silu_mul(x1, x2));
       }
-      const int row = m0 + mt * 16 + 4 * (ln >> 4) + r;
-      if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 16 + (ln & 15)] = f32_to_bf16_rne(silu_mul(x1, x2));
     }
     __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------------------
-// GEMM2 (+ routing weight), stream shape
-// ---------------------------------------------------------------------------
-constexpr int S2_SPLITK = 4;
-constexpr int S2_KPW = NB_I / S2_SPLITK;  // 4 K blocks per wave
-constexpr int S2_MT = 2;
+__global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T, int offset,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const int32_t* __restrict__ topk_ids,
+    const float* __restrict__ topk_w, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
+    float* __restrict__ perm_w, int32_t* __restrict__ tok_pair, uint16_t* __restrict__ c_act) {
+  __shared__ G1Shared sh;
+  dispatch_small(topk_ids, topk_w, T, offset, sh.d);
+  if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
+  const int total = sh.d.nact * D1_NT;
+  const int per = (total + gridDim.x - 1) / gridDim.x;
+  const int begin = blockIdx.x * per, end = min(total, begin + per);
+  const int kb0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * D1_KPW;
+  G1State st;
+  v8i a[D1_KPW], b0[D1_KPW], b1[D1_KPW];
+  if (begin < end) g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
+  for (int item = begin; item < end; item += 2) {
+    g1_item(item, item + 1 < end ? item + 1 : -1, a, b0, b1, st, sh, hidden, hscale, T, w13, s13, c_act);
+    if (item + 1 < end)
+      g1_item(item + 1, item + 2 < end ? item + 2 : -1, a, b1, b0, st, sh, hidden, hscale, T, w13, s13, c_act);
+  }
+}
 
-__global__ __launch_bounds__(64 * S2_SPLITK) void gemm2_stream_kernel(
+// ---------------------------------------------------------------------------
+// GEMM2 x routing weight + ordered combine, decode shape (T <= 64).
+//
+// One workgroup per 16-column tile of the output (448 tiles). Its work units
+// are (active expert, K half): each of the 8 waves takes units round-robin,
+// widens 8 K blocks of W2 (16 rows = the tile's columns) from e4m3 to bf16 and
+// runs the expert's rows through the bf16 MFMA. Each unit's 16 columns for each
+// of the expert's rows land in an LDS slab indexed by pair; then every token's
+// output is sum over its local experts in ascending id of (half0 + half1) * w,
+// rounded once to bf16 (zeros for tokens with no local expert). No partial
+// rows in memory and no separate combine kernel.
+// ---------------------------------------------------------------------------
+constexpr int D2_WAVES = 8;
+constexpr int D2_KPU = NB_I / 2;  // K blocks per unit (half of K)
+
+struct G2Shared {
+  int cnt[E_LOCAL];
+  int seg[E_LOCAL + 1];
+  int active[E_LOCAL];
+  int nact;
+  int pair[SMALL_P];
+  float pw[SMALL_P];
+  float slab[SMALL_P][2][16];
+};
+
+__global__ __launch_bounds__(64 * D2_WAVES, 4) void gemm2_combine_decode_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
-  __shared__ float red[S2_SPLITK][S2_MT][4][64];
-  const int slot = blockIdx.y;
-  if (slot >= hdr->n_active) return;
-  const int le = hdr->active[slot];
-  const int cnt = hdr->counts[le], seg = hdr->seg_start[le];
-  const int nt = blockIdx.x;  // output columns [16 nt, 16 nt + 16)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int col = lane & 15, kg = lane >> 4;
-  const int kb0 = wave * S2_KPW;
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, const int32_t* __restrict__ tok_pair,
+    int T, uint16_t* __restrict__ out) {
+  __shared__ G2Shared sh;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  if (tid < E_LOCAL) {
+    sh.cnt[tid] = hdr->counts[tid];
+    sh.seg[tid] = hdr->seg_start[tid];
+    sh.active[tid] = hdr->active[tid];
+  }
+  if (tid == 0) {
+    sh.seg[E_LOCAL] = hdr->seg_start[E_LOCAL];
+    sh.nact = hdr->n_active;
+  }
+  if (tid < T * TOP_K) sh.pair[tid] = tok_pair[tid];
+  __syncthreads();
+  const int P = sh.seg[E_LOCAL];
+  for (int p = tid; p < P; p += blockDim.x) sh.pw[p] = perm_w[p];
+  const int units = 2 * sh.nact;
 
-  const uint8_t* wrow = w2 + ((size_t)le * H + nt * 16 + col) * I + kg * 32;
-  const float* sw = s2 + ((size_t)le * NB_H + (nt * 16) / BLK) * NB_I;
-  v8i raw[S2_KPW];
+  for (int nt = blockIdx.x; nt < H / 16; nt += gridDim.x) {
+    for (int u = wave; u < units; u += D2_WAVES) {
+      const int le = sh.active[u >> 1], h = u & 1;
+      const int cnt = sh.cnt[le], seg = sh.seg[le];
+      const int kb0 = h * D2_KPU;
+      const uint8_t* wrow = w2 + ((size_t)le * H + nt * 16 + fr) * I + kb0 * BLK + kg * 32;
+      const float* sw = s2 + ((size_t)le * NB_H + (nt * 16) / BLK) * NB_I + kb0;
+      for (int m0 = 0; m0 < cnt; m0 += 16) {
+        const uint16_t* arow = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+        // two steps of 4 K blocks: activation rows (L2) first, then the weights
+#pragma unroll 1
+        for (int q = 0; q < D2_KPU; q += 4) {
+          v8bf a[4][4];
+          v8i raw[4];
 #pragma unroll
-  for (int kk = 0; kk < S2_KPW; ++kk) raw[kk] = load_v8i(wrow + (kb0 + kk) * BLK);
-
-  for (int m0 = 0; m0 < cnt; m0 += 16 * S2_MT) {
-    const uint16_t* arow[S2_MT];
+          for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-    for (int mt = 0; mt < S2_MT; ++mt)
-      arow[mt] = c_act + (size_t)(seg + min(m0 + mt * 16 + col, cnt - 1)) * I + kg * 32;
-    v4f acc[S2_MT];
+            for (int j = 0; j < 4; ++j) a[kk][j] = *reinterpret_cast<const v8bf*>(arow + (q + kk) * BLK + 8 * j);
 #pragma unroll
-    for (int mt = 0; mt < S2_MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int kk = 0; kk < 4; ++kk) raw[kk] = load_v8i(wrow + (q + kk) * BLK);
 #pragma unroll
-    for (int kk = 0; kk < S2_KPW; ++kk) {
-      const int kb = kb0 + kk;
-      const float s = sw[kb];
-      v8bf b[4];
+          for (int kk = 0; kk < 4; ++kk) {
+            v4f p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = fp8x8_to_bf16x8((uint32_t)raw[kk][2 * j], (uint32_t)raw[kk][2 * j + 1]);
+            for (int j = 0; j < 4; ++j)
+              p = mfma_bf16_k32(a[kk][j], fp8x8_to_bf16x8((uint32_t)raw[kk][2 * j], (uint32_t)raw[kk][2 * j + 1]), p);
+            const float s = sw[q + kk];
 #pragma unroll
-      for (int mt = 0; mt < S2_MT; ++mt) {
-        v4f p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v8bf a = *reinterpret_cast<const v8bf*>(arow[mt] + kb * BLK + 8 * j);
-          p = mfma_bf16_k32(a, b[j], p);
+            for (int r = 0; r < 4; ++r) acc[r] += p[r] * s;
+          }
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][r] += p[r] * s;
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + 4 * kg + r;
+          if (row < cnt) sh.slab[seg + row][h][fr] = acc[r];
+        }
       }
     }
-#pragma unroll
-    for (int mt = 0; mt < S2_MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][mt][r][lane] = acc[mt][r];
     __syncthreads();
+    for (int o = tid; o < T * 16; o += blockDim.x) {
+      const int t = o >> 4, c = o & 15;
+      float acc = 0.f;
 #pragma unroll
-    for (int q = 0; q < (S2_MT * 4 * 64) / (64 * S2_SPLITK); ++q) {
-      const int o = tid + q * 64 * S2_SPLITK;
-      const int mt = o >> 8, r = (o >> 6) & 3, ln = o & 63;
-      float x = 0.f;
-#pragma unroll
-      for (int w = 0; w < S2_SPLITK; ++w) x += red[w][mt][r][ln];
-      const int row = m0 + mt * 16 + 4 * (ln >> 4) + r;
-      if (row < cnt) partial[(size_t)(seg + row) * H + nt * 16 + (ln & 15)] = x * perm_w[seg + row];
+      for (int j = 0; j < TOP_K; ++j) {
+        const int p = sh.pair[t * TOP_K + j];
+        if (p >= 0) acc += (sh.slab[p][0][c] + sh.slab[p][1][c]) * sh.pw[p];
+      }
+      out[(size_t)t * H + nt * 16 + c] = f32_to_bf16_rne(acc);
     }
     __syncthreads();
   }
@@ -526,18 +601,32 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 namespace moe {
 
-hipError_t launch_gemm1_stream(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
-                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
-                               uint16_t* c_act, int max_active, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm1_stream_kernel, dim3(I / 16, max_active), dim3(64 * S1_SPLITK), 0, stream, hidden,
-                     hscale, T, w13, s13, hdr, perm_tok, c_act);
+int gemm1_decode_blocks_per_cu() {
+  static int cached = 0;
+  if (cached > 0) return cached;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm1_decode_kernel, 64 * D1_WAVES, 0) != hipSuccess || n < 1)
+    n = 1;
+  cached = n;
+  return n;
+}
+
+hipError_t launch_gemm1_decode(const uint8_t* hidden, const float* hscale, int T, int offset, const uint8_t* w13,
+                               const float* s13, const int32_t* topk_ids, const float* topk_w, DispatchHeader* hdr,
+                               int32_t* perm_tok, float* perm_w, int32_t* tok_pair, uint16_t* c_act, int grid,
+                               hipStream_t stream) {
+  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), 0, stream, hidden, hscale, T, offset, w13,
+                     s13, topk_ids, topk_w, hdr, perm_tok, perm_w, tok_pair, c_act);
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_stream(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
-                               const float* perm_w, float* partial, int max_active, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm2_stream_kernel, dim3(H / 16, max_active), dim3(64 * S2_SPLITK), 0, stream, c_act, w2,
-                     s2, hdr, perm_w, partial);
+hipError_t launch_gemm2_combine_decode(const uint16_t* c_act, const uint8_t* w2, const float* s2,
+                                       const DispatchHeader* hdr, const float* perm_w, const int32_t* tok_pair, int T,
+                                       uint16_t* out, int grid, hipStream_t stream) {
+  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm2_combine_decode_kernel, dim3(grid), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr,
+                     perm_w, tok_pair, T, out);
   return hipGetLastError();
 }
 

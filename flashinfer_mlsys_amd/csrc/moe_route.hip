@@ -3,38 +3,45 @@
 // route_kernel     -- reference moe/ref_moe.py:94-126 (sigmoid + bias, top-2-sum
 //                     group scores, top-4 of 8 groups, top-8 experts inside them,
 //                     weights from the unbiased sigmoid normalised over the 8 and
-//                     scaled). One wave64 per token, 4 experts per lane, 8 lanes
-//                     per 32-expert group; the choices are made with cross-lane
-//                     shuffles, no LDS.
+//                     scaled). One wave64 per token, 4 experts per lane; the
+//                     top-8 is a ballot/popcount threshold search (no serial
+//                     arg-max rounds).
 // dispatch_kernel  -- reference moe/ref_moe.py:131-145 (for each local expert the
 //                     ascending list of tokens that selected it). One workgroup
 //                     per local expert: a histogram of all local ids gives every
 //                     segment's start, then a ballot/popcount scan writes the
 //                     expert's tokens in ascending order. No atomics on global
 //                     memory, no host synchronisation.
+// dispatch_small_kernel -- the decode-size dispatch (T <= 64) in one workgroup.
 #include "moe_common.h"
+#include "moe_small_dispatch.h"
 
 namespace moe {
 
-// Selection key order: larger value first, lower expert id on equal values.
-__device__ __forceinline__ bool beats(float v, int i, float ov, int oi) {
-  return ov > v || (ov == v && oi < i);
+// Float -> unsigned key with the same order (larger float, larger key).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ float pick4(const float (&a)[4], int k) {
-  float r = a[0];
-  r = k == 1 ? a[1] : r;
-  r = k == 2 ? a[2] : r;
-  r = k == 3 ? a[3] : r;
-  return r;
-}
+__device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
-// Routes token t with the calling wave. Lanes 0..7 store slot `lane` of the
-// ascending selection: expert id, routing weight, and -1 into tok_pair (the
-// dispatch kernel overwrites the slots of local experts).
+// Routes token t with the calling wave (ref_moe.py:94-126). Lane l holds experts
+// 4l..4l+3, so the 8 lanes 8g..8g+7 hold routing group g.
+//  * scores: s = 1/(1+exp(-x)) with exp(-x) evaluated in fp64 and rounded once
+//    to fp32 (the correctly rounded value), IEEE fp32 division; sb = s + bias.
+//  * group score = sum of the two largest sb of the group (multiset top-2 merged
+//    over the group's 8 lanes); a group is kept when fewer than 4 groups beat it
+//    (larger score, or equal score and lower index).
+//  * the 8 experts are the 8 largest sb among the kept groups (others masked to
+//    the most negative finite float): the 8th largest key is found by a 32-step
+//    bitwise search on order-preserving keys with wave ballots + popcounts, then
+//    every key above it is taken plus the lowest-id keys equal to it.
+//  * weights = s / (sum of the 8 selected s + 1e-20) * rsf (unbiased s).
+// Writes, through generic pointers (global or LDS), the ascending selected ids
+// and their weights at ids[t*8 + pos], w[t*8 + pos]; tok_pair slots get -1.
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
-                                            int t, float rsf, int32_t* __restrict__ topk_ids,
-                                            float* __restrict__ topk_w, int32_t* __restrict__ tok_pair) {
+                                            int t, float rsf, int32_t* ids, float* wts, int32_t* tok_pair) {
   const int lane = threadIdx.x & 63;
   const float4 x4 = *reinterpret_cast<const float4*>(logits + (size_t)t * E_GLOBAL + 4 * lane);
   const uint2 b2 = *reinterpret_cast<const uint2*>(bias + 4 * lane);
@@ -44,15 +51,11 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
   float s[4], sb[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    // exp(-x) rounded once to fp32 (evaluated in fp64), then 1/(1+e) in fp32
-    // with IEEE division: the correctly rounded form of ref_moe.py:99.
     const float e = (float)exp(-(double)x[i]);
     s[i] = 1.0f / (1.0f + e);
     sb[i] = s[i] + b[i];
   }
 
-  // Group score = sum of the two largest biased scores of the 32-expert group
-  // (ref_moe.py:106-108). Multiset top-2 merged across the group's 8 lanes.
   float m1 = fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3]));
   float m2 = fmaxf(fminf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])),
                    fmaxf(fminf(sb[0], sb[1]), fminf(sb[2], sb[3])));
@@ -65,81 +68,63 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
     m2 = n2;
   }
   const float gscore = m1 + m2;
-
-  // Top-4 of the 8 group scores (ref_moe.py:110-114): keep a group when fewer
-  // than 4 groups beat it.
   const int g = lane >> 3;
-  int rank = 0;
+  int beaten = 0;
 #pragma unroll
   for (int j = 0; j < N_GROUP; ++j) {
-    const float oj = __shfl(gscore, j * 8);
-    rank += beats(gscore, g, oj, j) ? 1 : 0;
+    const float oj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), j * 8));
+    beaten += (oj > gscore || (oj == gscore && j < g)) ? 1 : 0;
   }
-  const bool keep = rank < TOPK_GROUP;
+  const bool keep = beaten < TOPK_GROUP;
 
-  // Top-8 of the biased scores inside the kept groups, others masked to the
-  // most negative finite float (ref_moe.py:116-119). Eight rounds of a
-  // wave-wide arg-max; the winner's lane retires that candidate.
-  float cand[4];
+  uint32_t key[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cand[i] = keep ? sb[i] : -3.402823466e+38f;
-  unsigned taken = 0;
-  int sel_id[TOP_K];
-  float sel_s[TOP_K];
-#pragma unroll
-  for (int r = 0; r < TOP_K; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (!(taken & (1u << i)) && beats(bv, bi, cand[i], 4 * lane + i)) {
-        bv = cand[i];
-        bi = 4 * lane + i;
-      }
-    }
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) {
-      const float ov = __shfl_xor(bv, k);
-      const int oi = __shfl_xor(bi, k);
-      if (beats(bv, bi, ov, oi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi >> 2) == lane) taken |= 1u << (bi & 3);
-    sel_id[r] = bi;
-    sel_s[r] = __shfl(pick4(s, bi & 3), bi >> 2);
+  for (int i = 0; i < 4; ++i) key[i] = order_key(keep ? sb[i] : -3.402823466e+38f);
+  uint32_t th = 0;
+#pragma unroll 4
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t trial = th | (1u << bit);
+    const int c = popc_ballot(key[0] >= trial) + popc_ballot(key[1] >= trial) + popc_ballot(key[2] >= trial) +
+                  popc_ballot(key[3] >= trial);
+    th = c >= TOP_K ? trial : th;
   }
-
-  // Ascending expert ids (the canonical order of a selected set).
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  bool sel[4], eq[4];
+  int n_gt = 0, eq_below = 0;
 #pragma unroll
-  for (int a = 1; a < TOP_K; ++a) {
+  for (int i = 0; i < 4; ++i) {
+    sel[i] = key[i] > th;
+    eq[i] = key[i] == th;
+    n_gt += popc_ballot(sel[i]);
+    eq_below += __popcll(__ballot(eq[i]) & lt);
+  }
+  const int need = TOP_K - n_gt;
 #pragma unroll
-    for (int c = a; c > 0; --c) {
-      if (sel_id[c] < sel_id[c - 1]) {
-        const int ti = sel_id[c]; sel_id[c] = sel_id[c - 1]; sel_id[c - 1] = ti;
-        const float ts = sel_s[c]; sel_s[c] = sel_s[c - 1]; sel_s[c - 1] = ts;
-      }
+  for (int i = 0; i < 4; ++i) {
+    if (eq[i]) {
+      sel[i] = eq_below < need;
+      ++eq_below;
     }
   }
-  // Weights from the unbiased scores over all 8 selected experts (ref_moe.py:121-126).
-  float sum = 0.f;
+  int pos = 0;
+  float ssum = 0.f;
 #pragma unroll
-  for (int r = 0; r < TOP_K; ++r) sum += sel_s[r];
-  const float denom = sum + 1e-20f;
-
-  if (lane < TOP_K) {
-    int my_id = sel_id[0];
-    float my_s = sel_s[0];
-#pragma unroll
-    for (int r = 1; r < TOP_K; ++r) {
-      my_id = lane == r ? sel_id[r] : my_id;
-      my_s = lane == r ? sel_s[r] : my_s;
-    }
-    topk_ids[(size_t)t * TOP_K + lane] = my_id;
-    topk_w[(size_t)t * TOP_K + lane] = (my_s / denom) * rsf;
-    if (tok_pair) tok_pair[(size_t)t * TOP_K + lane] = -1;
+  for (int i = 0; i < 4; ++i) {
+    pos += __popcll(__ballot(sel[i]) & lt);
+    ssum += sel[i] ? s[i] : 0.f;
   }
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) ssum += __shfl_xor(ssum, k);
+  const float denom = ssum + 1e-20f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (sel[i]) {
+      ids[(size_t)t * TOP_K + pos] = 4 * lane + i;
+      wts[(size_t)t * TOP_K + pos] = (s[i] / denom) * rsf;
+      ++pos;
+    }
+  }
+  if (tok_pair && lane < TOP_K) tok_pair[(size_t)t * TOP_K + lane] = -1;
 }
 
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
@@ -226,6 +211,20 @@ __global__ __launch_bounds__(256) void dispatch_kernel(const int32_t* __restrict
   }
 }
 
+
+// Dispatch of up to 64 tokens in one workgroup with the same device code the
+// decode GEMM1 kernel runs in each of its workgroups (dispatch tap).
+__global__ __launch_bounds__(SMALL_P) void dispatch_small_kernel(const int32_t* __restrict__ topk_ids,
+                                                                 const float* __restrict__ topk_w, int T, int offset,
+                                                                 DispatchHeader* __restrict__ hdr,
+                                                                 int32_t* __restrict__ perm_tok,
+                                                                 float* __restrict__ perm_w,
+                                                                 int32_t* __restrict__ tok_pair) {
+  __shared__ SmallDispatch d;
+  dispatch_small(topk_ids, topk_w, T, offset, d);
+  store_small_dispatch(d, T, hdr, perm_tok, perm_w, tok_pair);
+}
+
 }  // namespace moe
 
 // ---------------------------------------------------------------------------
@@ -238,6 +237,15 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, int T, float 
   if (T <= 0) return hipSuccess;
   hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias, T, rsf, topk_ids,
                      topk_w, tok_pair);
+  return hipGetLastError();
+}
+
+hipError_t launch_dispatch_small(const int32_t* topk_ids, const float* topk_w, int T, int offset,
+                                 DispatchHeader* hdr, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
+                                 hipStream_t stream) {
+  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(SMALL_P), 0, stream, topk_ids, topk_w, T, offset, hdr,
+                     perm_tok, perm_w, tok_pair);
   return hipGetLastError();
 }
 

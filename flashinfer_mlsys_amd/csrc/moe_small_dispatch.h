@@ -1,0 +1,107 @@
+// Dispatch of up to 64 tokens inside one workgroup's LDS (reference
+// moe/ref_moe.py:131-145): per local expert, the ascending list of tokens that
+// selected it, the pair weights and each (token, slot)'s pair index.
+//
+// With T <= 64 one token fits one lane, so a 32-bit local-expert mask per token
+// turns every expert's token list into one wave ballot: its popcount is the
+// expert's count and the popcount below a lane is that token's rank. Used by the
+// decode GEMM1 kernel (each workgroup derives the dispatch itself, so no header
+// has to be read back from memory before the weight stream starts) and by the
+// dispatch tap kernel.
+#pragma once
+
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int SMALL_T = 64;
+constexpr int SMALL_P = SMALL_T * TOP_K;
+
+struct SmallDispatch {
+  int cnt[E_LOCAL];
+  int seg[E_LOCAL + 1];
+  int nact;
+  int active[E_LOCAL];
+  int ids[SMALL_P];    // routed global ids, [T, 8] ascending per token
+  float wts[SMALL_P];  // their routing weights
+  int tok[SMALL_P];    // pair -> token
+  float pw[SMALL_P];   // pair -> routing weight
+  int pair[SMALL_P];   // (token, slot) -> pair, -1 if the slot's expert is not local
+  uint32_t mask[SMALL_T];
+};
+
+// Called by every thread of the workgroup; blockDim.x must be a multiple of 64
+// and at least SMALL_P. T <= SMALL_T.
+__device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, const float* __restrict__ wts,
+                                               int T, int offset, SmallDispatch& d) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  if (tid < SMALL_T) d.mask[tid] = 0u;
+  if (tid < T * TOP_K) {
+    d.ids[tid] = ids[tid];
+    d.wts[tid] = wts[tid];
+  }
+  __syncthreads();
+  if (tid < T * TOP_K) {
+    const unsigned le = (unsigned)(d.ids[tid] - offset);
+    if (le < (unsigned)E_LOCAL) atomicOr(&d.mask[tid >> 3], 1u << le);
+    d.pair[tid] = -1;
+  }
+  __syncthreads();
+  for (int le = wave; le < E_LOCAL; le += nw) {
+    const unsigned long long m = __ballot(lane < T && ((d.mask[lane] >> le) & 1u));
+    if (lane == 0) d.cnt[le] = __popcll(m);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, nact = 0;
+    for (int e = 0; e < E_LOCAL; ++e) {
+      d.seg[e] = acc;
+      if (d.cnt[e] > 0) d.active[nact++] = e;
+      acc += d.cnt[e];
+    }
+    d.seg[E_LOCAL] = acc;
+    d.nact = nact;
+    for (int e = nact; e < E_LOCAL; ++e) d.active[e] = -1;
+  }
+  __syncthreads();
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int le = wave; le < E_LOCAL; le += nw) {
+    const bool has = lane < T && ((d.mask[lane] >> le) & 1u);
+    const unsigned long long m = __ballot(has);
+    if (has) {
+      const int pos = d.seg[le] + __popcll(m & lt);
+      int slot = 0;
+#pragma unroll
+      for (int j = 0; j < TOP_K; ++j) slot = d.ids[lane * TOP_K + j] == offset + le ? j : slot;
+      d.tok[pos] = lane;
+      d.pw[pos] = d.wts[lane * TOP_K + slot];
+      d.pair[lane * TOP_K + slot] = pos;
+    }
+  }
+  __syncthreads();
+}
+
+// Writes the dispatch to memory in the layout of dispatch_kernel (header,
+// perm_tok, perm_w, tok_pair). Called by every thread of one workgroup.
+__device__ __forceinline__ void store_small_dispatch(const SmallDispatch& d, int T, DispatchHeader* __restrict__ hdr,
+                                                     int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,
+                                                     int32_t* __restrict__ tok_pair) {
+  const int tid = threadIdx.x;
+  if (tid < E_LOCAL) {
+    hdr->counts[tid] = d.cnt[tid];
+    hdr->seg_start[tid] = d.seg[tid];
+    hdr->active[tid] = d.active[tid];
+  }
+  if (tid == 0) {
+    hdr->seg_start[E_LOCAL] = d.seg[E_LOCAL];
+    hdr->n_active = d.nact;
+  }
+  const int P = d.seg[E_LOCAL];
+  for (int p = tid; p < P; p += blockDim.x) {
+    perm_tok[p] = d.tok[p];
+    perm_w[p] = d.pw[p];
+  }
+  for (int i = tid; i < T * TOP_K; i += blockDim.x) tok_pair[i] = d.pair[i];
+}
+
+}  // namespace moe

@@ -66,18 +66,22 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
                     void* stream);
 
 /*
- * moe_fp8_forward plus six caller-created hipEvent_t handles recorded on
- * `stream` around the stages: events[0] before routing, [1] before dispatch,
- * [2] before GEMM1+SwiGLU, [3] before GEMM2, [4] before the combine, [5] after.
- * No reference counterpart (the reference timed its stages with torch.profiler,
- * scripts/ncu_profile.py:89-143); used by bench.py for per-kernel durations.
+ * Runs one stage of moe_fp8_forward with the same arguments, reading and
+ * writing the workspace as the forward does: 0 = routing (+ dispatch for
+ * T > 64), 1 = GEMM1 + SwiGLU (+ the in-workgroup dispatch for T <= 64),
+ * 2 = GEMM2 x routing weight (+ the ordered combine for T <= 64), 3 = the
+ * combine (T > 64; nothing for T <= 64). A stage's inputs must already be in
+ * the workspace (a moe_fp8_forward with the same arguments ran on it). No
+ * reference counterpart (the reference timed its stages with torch.profiler,
+ * scripts/ncu_profile.py:89-143): the benchmark times each kernel over many
+ * back-to-back launches of its stage.
  */
-int moe_fp8_forward_timed(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
-                          const float* hidden_states_scale, const uint8_t* gemm1_weights,
-                          const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
-                          const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
-                          double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
-                          void* stream, void* const* events);
+int moe_fp8_run_stage(int stage, const float* routing_logits, const uint16_t* routing_bias,
+                      const uint8_t* hidden_states, const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                      const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                      const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                      double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /*
  * Routing stage alone (reference moe/ref_moe.py:94-126; the sigmoid/bias kernel
@@ -104,8 +108,22 @@ int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int
 int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, int64_t local_expert_offset,
                      int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair, void* stream);
 
-/* Expert-GEMM shape used by moe_fp8_forward: 0 = by token count (default),
- * 1 = always the decode (stream) shape, 2 = always the prefill (tiled) shape.
+/*
+ * Routing and dispatch as moe_fp8_forward runs them (for T <= 64 the routing
+ * kernel plus, in one workgroup, the dispatch code every decode GEMM1
+ * workgroup runs; otherwise the two kernels above), writing
+ * topk_ids / topk_w [T, 8], header [128], perm_tok / perm_w [8T] and
+ * tok_pair [T, 8] (fully written: -1 for non-local slots). Parity tap for
+ * reference moe/ref_moe.py:94-145.
+ */
+int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
+                           int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
+                           float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
+                           void* stream);
+
+/* Kernel shape used by moe_fp8_forward: 0 = by token count (default: the
+ * decode shape for T <= 64, the prefill shape above), 1 = the same as 0
+ * (the decode shape exists only for T <= 64), 2 = always the prefill shape.
  * Process-global; meant for tests. Returns the previous value. */
 int moe_fp8_set_path(int path);
 

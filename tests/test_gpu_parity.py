@@ -88,10 +88,7 @@ def test_route_selection_bit_exact(case):
     np.testing.assert_allclose(w.cpu().numpy(), ref_w, rtol=4e-7 * 8, atol=0)
 
 
-@pytest.mark.parametrize("case", ALL, indirect=True)
-def test_dispatch_bit_exact(case):
-    ids, w, pair = fm.route(case.gpu[0], case.gpu[1], case.rsf)
-    header, perm_tok, perm_w, pair = fm.dispatch(ids, w, pair, case.offset)
+def _check_dispatch(case, ids, w, header, perm_tok, perm_w, pair):
     h = header.cpu().numpy()
     counts, seg = h[:32], h[32:65]
     np.testing.assert_array_equal(counts, case.g["counts"])
@@ -102,14 +99,33 @@ def test_dispatch_bit_exact(case):
     np.testing.assert_array_equal(h[66:66 + n_act], np.nonzero(counts)[0])
     # perm_w is the routing weight of each pair; tok_pair points back at it
     ids_c, w_c, pair_c = ids.cpu().numpy(), w.cpu().numpy(), pair.cpu().numpy()
+    np.testing.assert_array_equal(ids_c, case.g["sel_ids"].astype(np.int32))
     pt, pw = perm_tok.cpu().numpy()[:P], perm_w.cpu().numpy()[:P]
     local = (ids_c >= case.offset) & (ids_c < case.offset + 32)
     assert ((pair_c >= 0) == local).all()
+    assert (pair_c[~local] == -1).all()
     t_idx, j_idx = np.nonzero(local)
     p_idx = pair_c[t_idx, j_idx]
     assert sorted(p_idx.tolist()) == list(range(P))
     np.testing.assert_array_equal(pt[p_idx], t_idx)
     np.testing.assert_array_equal(pw[p_idx], w_c[t_idx, j_idx])
+
+
+@pytest.mark.parametrize("case", ALL, indirect=True)
+def test_dispatch_bit_exact(case):
+    """The two separate stage kernels (route_kernel, dispatch_kernel)."""
+    ids, w, pair = fm.route(case.gpu[0], case.gpu[1], case.rsf)
+    header, perm_tok, perm_w, pair = fm.dispatch(ids, w, pair, case.offset)
+    _check_dispatch(case, ids, w, header, perm_tok, perm_w, pair)
+
+
+@pytest.mark.parametrize("case", ALL, indirect=True)
+def test_route_dispatch_as_forward_runs_it(case):
+    """Routing + dispatch exactly as the forward runs them (one fused kernel for T <= 64)."""
+    ids, w, header, perm_tok, perm_w, pair = fm.route_dispatch(case.gpu[0], case.gpu[1], case.offset, case.rsf)
+    _check_dispatch(case, ids, w, header, perm_tok, perm_w, pair)
+    ids2, w2, _ = fm.route(case.gpu[0], case.gpu[1], case.rsf)
+    assert torch.equal(ids, ids2) and torch.equal(w, w2)
 
 
 @pytest.mark.parametrize("case", ALL, indirect=True)
@@ -131,9 +147,10 @@ def test_forward_matches_reference(case):
     assert (out_np[~has] == 0).all()
 
 
-@pytest.mark.parametrize("case", ["t16", "decode_t64", "prefill_t1024"], indirect=True)
+@pytest.mark.parametrize("case", ["decode_t1", "t16", "decode_t64"], indirect=True)
 def test_decode_and_prefill_shapes_agree(case):
-    old = fm.set_path(1)
+    """T <= 64 runs the decode kernels by default; path 2 forces the prefill kernels."""
+    old = fm.set_path(0)
     try:
         a = case.forward().float()
         fm.set_path(2)
@@ -156,7 +173,7 @@ def test_deterministic(case):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize("case", ["prefill_t8192"], indirect=True)
+@pytest.mark.parametrize("case", ["decode_t64", "prefill_t8192"], indirect=True)
 def test_token_permutation_equivariance(case):
     """Each token's output depends only on its own row: permuting tokens permutes rows, bit for bit."""
     T = case.w.T
@@ -201,3 +218,24 @@ def test_dps_writes_into_output(case):
     assert ret is None
     ref = bf16_bits_to_f32(case.g["out_bf16"])
     assert_close_bf16(out.float().cpu().numpy()[case.g["out_rows"]], ref, "dps")
+
+
+@pytest.mark.parametrize("case", ["decode_t1", "t16", "prefill_t1024"], indirect=True)
+def test_graph_replay_matches_eager(case):
+    """The forward captured in a HIP graph: every replay, with eager work and
+    synchronisations between replays, gives the eager output bit for bit."""
+    out = torch.empty((case.w.T, 7168), dtype=torch.bfloat16, device=case.gpu[0].device)
+    ws = torch.empty(fm.workspace_size(case.w.T), dtype=torch.uint8, device=out.device)
+    fm.kernel(*case.gpu, case.offset, case.rsf, out, workspace=ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fm.kernel(*case.gpu, case.offset, case.rsf, out, workspace=ws)
+    for i in range(3):
+        out.fill_(3.0)
+        other = case.forward()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+        assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
