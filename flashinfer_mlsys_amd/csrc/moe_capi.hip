@@ -154,7 +154,7 @@ hipError_t run_stage(int stage, const Call& c) {
                                    c.perm_tok, c.perm_w, c.tok_pair, c.c_act, grid, c.stream);
       }
       return launch_gemm1_tiled(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
-                                (cu_count() * 2 + 7) / 8 * 8, c.stream);
+                                (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
       if (c.decode)
         return launch_gemm2_combine_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.tok_pair, c.T, c.out, H / 16,

@@ -322,71 +322,98 @@ __device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM1 + SwiGLU, tiled shape: 128 rows x 64 pair columns (128 W13 rows) per item.
-// 4 waves as 2 (rows) x 2 (pair columns); each wave 64 rows x 32 pair columns.
+// GEMM1 + SwiGLU, prefill shape: 128 rows x 128 column pairs (X1 rows n..n+127
+// and X2 rows 2048+n..) per item, 8 waves as 2 (rows) x 4 (pairs); each wave
+// owns 64 rows x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles).
+//
+// Operands go global -> LDS with the direct load (global_load_lds_dwordx4):
+// one wave instruction moves 64 lanes x 16 B and lane l's bytes land at
+// base + 16 l, so the LDS holds every 16 x 128 e4m3 fragment in the order the
+// MFMA reads it and each fragment read is a linear 1 KB ds_read_b128 (no bank
+// conflicts, no staging registers). Lane l of a fragment half h carries K
+// bytes h*64 + (l/16)*16 .. +16 of row l%16 (the same K order for A and B, so
+// the products pair up). The activation scales of the item's rows ride along.
+// Three LDS stages: the loads for K block kb+2 are issued while kb computes.
 // ---------------------------------------------------------------------------
-constexpr int T1_BM = 128;
-constexpr int T1_BNP = 64;
-constexpr int T1_LDS = 144;  // bytes per staged 128-byte K row (+16 keeps 16 rows on distinct banks)
-constexpr int T1_NT = I / T1_BNP;
+constexpr int FRAG_BYTES = 2048;           // one 16 x 128 e4m3 fragment
+constexpr int Q1_BM = 128;
+constexpr int Q1_BNP = 128;
+constexpr int Q1_WAVES = 8;
+constexpr int Q1_NT = I / Q1_BNP;          // 16 column-pair tiles
+constexpr int Q1_AFR = Q1_BM / 16;         // 8 activation fragments per stage
+constexpr int Q1_BFR = 2 * Q1_BNP / 16;    // 16 weight fragments per stage (0-7 X1, 8-15 X2)
+constexpr int Q1_JOBS = 2 * (Q1_AFR + Q1_BFR) / Q1_WAVES;  // fragment halves per wave per stage: 6
+constexpr int Q1_SCALE_OFF = (Q1_AFR + Q1_BFR) * FRAG_BYTES;
+constexpr int Q1_STAGE = Q1_SCALE_OFF + Q1_BM * 4;
+constexpr int Q1_NSTAGE = 3;
+static_assert(2 * (Q1_AFR + Q1_BFR) % Q1_WAVES == 0, "even job split");
 
-__global__ __launch_bounds__(256, 2) void gemm1_tiled_kernel(
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void lds_direct16(const void* gsrc, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_direct4(const void* gsrc, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 4, 0, 0);
+}
+__device__ __forceinline__ v8i lds_frag(const uint8_t* f) {
+  const int lane = threadIdx.x & 63;
+  const v4i lo = *reinterpret_cast<const v4i*>(f + lane * 16);
+  const v4i hi = *reinterpret_cast<const v4i*>(f + 1024 + lane * 16);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+__global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
     const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][T1_BM * T1_LDS];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][2 * T1_BNP * T1_LDS];
-  __shared__ __attribute__((aligned(16))) float sSa[2][T1_BM];
-  __shared__ int sTok[T1_BM];
+  extern __shared__ __attribute__((aligned(16))) uint8_t q1_lds[];
+  __shared__ int sTok[Q1_BM];
   __shared__ TileMap map;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  const int fr = lane & 15, kg = lane >> 4;
-  build_tile_map<T1_BM>(hdr, map);
+  build_tile_map<Q1_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = total_m * T1_NT;
+  const int total = total_m * Q1_NT;
 
   for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
     const int nt = item / total_m, mg = item % total_m;
     const int e = find_expert(map, mg);
-    const int m0 = (mg - map.mt_prefix[e]) * T1_BM;
+    const int m0 = (mg - map.mt_prefix[e]) * Q1_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
-    const int valid = min(T1_BM, cnt - m0);
-    if (tid < T1_BM) sTok[tid] = perm_tok[seg + m0 + min(tid, valid - 1)];
+    const int valid = min(Q1_BM, cnt - m0);
+    if (tid < Q1_BM) sTok[tid] = perm_tok[seg + m0 + min(tid, valid - 1)];
     __syncthreads();
 
-    const uint8_t* a_src[4];
-    const uint8_t* b_src[4];
-    int lds_off[4];
+    // This wave's load jobs: fragment halves j = wave*6 + i of the 48 per stage.
+    const uint8_t* src[Q1_JOBS];
+    int dst[Q1_JOBS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      a_src[i] = hidden + (size_t)sTok[row] * H + ch * 16;
-      const int wr = row < T1_BNP ? nt * T1_BNP + row : I + nt * T1_BNP + (row - T1_BNP);
-      b_src[i] = w13 + ((size_t)e * N1 + wr) * H + ch * 16;
-      lds_off[i] = row * T1_LDS + ch * 16;
+    for (int i = 0; i < Q1_JOBS; ++i) {
+      const int j = wave * Q1_JOBS + i, f = j >> 1, h = j & 1;
+      const int koff = h * 64 + kg * 16;
+      if (f < Q1_AFR) {
+        src[i] = hidden + (size_t)sTok[f * 16 + fr] * H + koff;
+      } else {
+        const int g = f - Q1_AFR;
+        const int row = g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 + fr : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16 + fr;
+        src[i] = w13 + ((size_t)e * N1 + row) * H + koff;
+      }
+      dst[i] = f * FRAG_BYTES + h * 1024;
     }
-    const int my_tok = tid < T1_BM ? sTok[tid] : 0;
-    const float* su = s13 + ((size_t)e * NB_N1 + (nt * T1_BNP) / BLK) * NB_H;
-    const float* sg = s13 + ((size_t)e * NB_N1 + (I + nt * T1_BNP) / BLK) * NB_H;
+    const float* ssrc = hscale + sTok[wave * 16 + (lane & 15)];
+    const float* su = s13 + ((size_t)e * NB_N1 + nt) * NB_H;          // X1 block row nt
+    const float* sg = s13 + ((size_t)e * NB_N1 + NB_I + nt) * NB_H;   // X2 block row 16 + nt
 
-    v4i ra[4], rb[4];
-    float rsa = 0.f;
-    auto gload = [&](int kb) {
+    auto issue = [&](int kb) {
+      uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ra[i] = *reinterpret_cast<const v4i*>(a_src[i] + kb * BLK);
-        rb[i] = *reinterpret_cast<const v4i*>(b_src[i] + kb * BLK);
-      }
-      if (tid < T1_BM) rsa = hscale[(size_t)kb * T + my_tok];
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<v4i*>(&sA[buf][lds_off[i]]) = ra[i];
-        *reinterpret_cast<v4i*>(&sB[buf][lds_off[i]]) = rb[i];
-      }
-      if (tid < T1_BM) sSa[buf][tid] = rsa;
+      for (int i = 0; i < Q1_JOBS; ++i) lds_direct16(src[i] + kb * BLK, st + dst[i]);
+      if (lane < 16) lds_direct4(ssrc + (size_t)kb * T, st + Q1_SCALE_OFF + wave * 64);
     };
 
     v4f accu[4][2], accg[4][2];
@@ -395,40 +422,49 @@ __global__ __launch_bounds__(256, 2) void gemm1_tiled_kernel(
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
+    issue(0);
+    issue(1);
+#pragma unroll 1
     for (int kb = 0; kb < NB_H; ++kb) {
-      const int buf = kb & 1;
-      if (kb + 1 < NB_H) gload(kb + 1);
+      // this wave's loads for K block kb are done (the next stage's 7 may still fly)
+      if (kb + 1 < NB_H) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // every wave's loads for kb landed; kb-1 is fully read
+      asm volatile("" ::: "memory");
+      if (kb + 2 < NB_H) issue(kb + 2);
+      const uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
       const float swu = su[kb], swg = sg[kb];
-      v8i a[4], bu[2], bg[2];
+      // MFMA phase: all 16 products of this K block into their own registers ...
+      v8i a[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) a[mt] = load_v8i(&sA[buf][(wm * 64 + mt * 16 + fr) * T1_LDS + kg * 32]);
+      for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag(st + (wm * 4 + mt) * FRAG_BYTES);
+      v4f pu[4][2], pg[4][2];
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) {
-        bu[n2] = load_v8i(&sB[buf][(wn * 32 + n2 * 16 + fr) * T1_LDS + kg * 32]);
-        bg[n2] = load_v8i(&sB[buf][(T1_BNP + wn * 32 + n2 * 16 + fr) * T1_LDS + kg * 32]);
+        const v8i bu = lds_frag(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES);
+        const v8i bg = lds_frag(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          pu[mt][n2] = mfma_fp8_k128(a[mt], bu);
+          pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
+        }
       }
+      // ... then the fp32 block-scale FMAs (overlap the other wave's MFMA phase).
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const v4f sa = *reinterpret_cast<const v4f*>(&sSa[buf][wm * 64 + mt * 16 + 4 * kg]);
+        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
         v4f fu, fg;
 #pragma unroll
         for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
 #pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2) {
-          const v4f pu = mfma_fp8_k128(a[mt], bu[n2]);
-          const v4f pg = mfma_fp8_k128(a[mt], bg[n2]);
+        for (int n2 = 0; n2 < 2; ++n2)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            accu[mt][n2][r] += pu[r] * fu[r];
-            accg[mt][n2][r] += pg[r] * fg[r];
+            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
+            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
           }
-        }
       }
-      if (kb + 1 < NB_H) lstore(buf ^ 1);
-      __syncthreads();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -438,10 +474,11 @@ __global__ __launch_bounds__(256, 2) void gemm1_tiled_kernel(
         for (int r = 0; r < 4; ++r) {
           const int row = m0 + wm * 64 + mt * 16 + 4 * kg + r;
           if (row < cnt) {
-            const int col = nt * T1_BNP + wn * 32 + n2 * 16 + fr;
+            const int col = nt * Q1_BNP + wn * 32 + n2 * 16 + fr;
             c_act[(size_t)(seg + row) * I + col] = f32_to_bf16_rne(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
           }
         }
+    __syncthreads();  // all waves are done with the LDS stages and sTok
   }
 }
 
@@ -633,8 +670,15 @@ hipError_t launch_gemm2_combine_decode(const uint16_t* c_act, const uint8_t* w2,
 hipError_t launch_gemm1_tiled(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
                               uint16_t* c_act, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm1_tiled_kernel, dim3(grid), dim3(256), 0, stream, hidden, hscale, T, w13, s13, hdr,
-                     perm_tok, c_act);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_tiled_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * Q1_STAGE);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(gemm1_tiled_kernel, dim3(grid), dim3(64 * Q1_WAVES), Q1_NSTAGE * Q1_STAGE, stream, hidden,
+                     hscale, T, w13, s13, hdr, perm_tok, c_act);
   return hipGetLastError();
 }
 
