@@ -159,7 +159,7 @@ hipError_t run_stage(int stage, const Call& c) {
       if (c.decode)
         return launch_gemm2_combine_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.tok_pair, c.T, c.out, H / 16,
                                            c.stream);
-      return launch_gemm2_tiled(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() * 2 + 7) / 8 * 8,
+      return launch_gemm2_tiled(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() + 7) / 8 * 8,
                                 c.stream);
     case 3:
       if (c.decode) return hipSuccess;

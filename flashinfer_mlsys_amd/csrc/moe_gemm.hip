@@ -483,122 +483,148 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2 (+ routing weight), tiled shape: 128 rows x 128 output columns per item,
-// K staged 64 at a time (half a scale block). 4 waves as 2 x 2 of 64 x 64.
+// GEMM2 (+ routing weight), prefill shape: 128 rows x 256 output columns per
+// item on the bf16 MFMA v_mfma_f32_32x32x16_bf16 (full bf16 rate; the 16x16x32
+// form runs at well under half of it), 8 waves as 2 (rows) x 4 (columns), each
+// 64 x 64 = 2 x 2 tiles of 32 x 32.
+//
+// Both operands arrive by direct global -> LDS loads into a 4-slot ring, three
+// 64-wide K stages ahead of the MFMAs, so no load waits in registers. In LDS a
+// W2 block (32 rows x 32 K, e4m3) holds in lane l's 16 B row l % 32, K
+// 16 (l / 32) + [0, 16); each lane reads its 16 B linearly and widens them
+// exactly to bf16 as two MFMA steps: step t takes K 16 g + 8 t + [0, 8) in lane
+// group g = l / 32. The activation fragments (bf16 SwiGLU output) are loaded
+// in that same K order, which the MFMA sum does not see. The fp32 weight-block
+// scale is applied once per 128-wide K block.
 // ---------------------------------------------------------------------------
-constexpr int T2_BM = 128;
-constexpr int T2_BN = 128;
-constexpr int T2_BK = 64;
-constexpr int T2_LDS = 144;  // bytes per staged row of 64 bf16 (+16)
-constexpr int T2_NT = H / T2_BN;
-constexpr int T2_NK = I / T2_BK;  // 32 stages
+constexpr int Q2_BM = 128;
+constexpr int Q2_BN = 256;
+constexpr int Q2_WAVES = 8;
+constexpr int Q2_NT = H / Q2_BN;      // 28 column tiles
+constexpr int Q2_KS = 64;             // K per stage
+constexpr int Q2_NS = I / Q2_KS;      // 32 stages
+constexpr int Q2_FRAG = 1024;         // 64 lanes x 16 B
+constexpr int Q2_A_BYTES = Q2_BM * Q2_KS * 2;  // 16 KB: 4 row blocks x 2 spans x 2 steps
+constexpr int Q2_B_BYTES = Q2_BN * Q2_KS;      // 16 KB: 8 row blocks x 2 spans
+constexpr int Q2_STAGE = Q2_A_BYTES + Q2_B_BYTES;
+constexpr int Q2_NSTAGE = 4;
+static_assert(Q2_NS % Q2_NSTAGE == 0, "the last stage's slot must not be one the next item's prologue fills");
 
-__global__ __launch_bounds__(256, 2) void gemm2_tiled_kernel(
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f mfma_bf16_32x32x16(const v8bf& a, const v8bf& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int q2_afrag(int blk, int span, int t) { return ((blk * 2 + span) * 2 + t) * Q2_FRAG; }
+__device__ __forceinline__ int q2_bfrag(int blk, int span) { return Q2_A_BYTES + (blk * 2 + span) * Q2_FRAG; }
+
+__global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][T2_BM * T2_LDS];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][T2_BN * T2_LDS];
+  extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
   __shared__ TileMap map;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  const int fr = lane & 15, kg = lane >> 4;
-  build_tile_map<T2_BM>(hdr, map);
+  const int lr = lane & 31, lg = lane >> 5;
+  build_tile_map<Q2_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = total_m * T2_NT;
+  const int total = total_m * Q2_NT;
 
   for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
     const int nt = item / total_m, mg = item % total_m;
     const int e = find_expert(map, mg);
-    const int m0 = (mg - map.mt_prefix[e]) * T2_BM;
+    const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
 
-    const uint8_t* a_src[4];
-    int a_off[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      const int r = seg + min(m0 + row, cnt - 1);
-      a_src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)r * I) + ch * 16;
-      a_off[i] = row * T2_LDS + ch * 16;
-    }
-    const uint8_t* b_src[2];
-    int b_off[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i, row = c >> 2, ch = c & 3;
-      b_src[i] = w2 + ((size_t)e * H + nt * T2_BN + row) * I + ch * 16;
-      b_off[i] = row * T2_LDS + ch * 32;
-    }
-    const float* sw = s2 + ((size_t)e * NB_H + (nt * T2_BN) / BLK) * NB_I;
+    // Per stage each wave issues 2 activation loads (row block wave / 2, span
+    // wave & 1, steps 0 and 1) and 2 weight loads (row block wave, spans 0, 1).
+    const int ablk = wave >> 1, aspan = wave & 1;
+    const int arow = seg + min(m0 + ablk * 32 + lr, cnt - 1);
+    const uint8_t* asrc = reinterpret_cast<const uint8_t*>(c_act + (size_t)arow * I + aspan * 32 + lg * 16);
+    const uint8_t* bsrc = w2 + ((size_t)e * H + nt * Q2_BN + wave * 32 + lr) * I + lg * 16;
+    const float* swp = s2 + ((size_t)e * NB_H + (nt * Q2_BN + wn * 64) / BLK) * NB_I;
 
-    v4i ra[4], rb[2];
-    auto gload = [&](int kk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const v4i*>(a_src[i] + kk * T2_BK * 2);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const v4i*>(b_src[i] + kk * T2_BK);
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<v4i*>(&sA[buf][a_off[i]]) = ra[i];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const v8bf lo = fp8x8_to_bf16x8((uint32_t)rb[i][0], (uint32_t)rb[i][1]);
-        const v8bf hi = fp8x8_to_bf16x8((uint32_t)rb[i][2], (uint32_t)rb[i][3]);
-        *reinterpret_cast<v8bf*>(&sB[buf][b_off[i]]) = lo;
-        *reinterpret_cast<v8bf*>(&sB[buf][b_off[i] + 16]) = hi;
-      }
+    auto issue = [&](int s) {
+      uint8_t* st = q2_lds + (s % Q2_NSTAGE) * Q2_STAGE;
+      const uint8_t* as = asrc + s * Q2_KS * 2;
+      lds_direct16(as, st + q2_afrag(ablk, aspan, 0));
+      lds_direct16(as + 16, st + q2_afrag(ablk, aspan, 1));
+      const uint8_t* bs = bsrc + s * Q2_KS;
+      lds_direct16(bs, st + q2_bfrag(wave, 0));
+      lds_direct16(bs + 32, st + q2_bfrag(wave, 1));
     };
 
-    v4f acc[4][4];
+    v16f acc[2][2], p[2][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int n4 = 0; n4 < 4; ++n4) acc[mt][n4] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 2; ++j) { acc[i][j] = v16f{}; p[i][j] = v16f{}; }
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kk = 0; kk < T2_NK; ++kk) {
-      const int buf = kk & 1;
-      if (kk + 1 < T2_NK) gload(kk + 1);
-      const float s = sw[kk >> 1];
-      v8bf a[4][2], b[4][2];
+    issue(0);
+    issue(1);
+    issue(2);
+#pragma unroll 1
+    for (int s = 0; s < Q2_NS; ++s) {
+      // stage s has landed for this wave (stages s+1, s+2 may still fly) ...
+      if (s + 2 < Q2_NS) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else if (s + 1 < Q2_NS) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // ... and for every wave; every wave is also done reading stage s-1's slot
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (s + 3 < Q2_NS) issue(s + 3);
+
+      const uint8_t* st = q2_lds + (s % Q2_NSTAGE) * Q2_STAGE;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int u = 0; u < 2; ++u) {
+        v8bf bf[2][2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          a[mt][j] = *reinterpret_cast<const v8bf*>(&sA[buf][(wm * 64 + mt * 16 + fr) * T2_LDS + kg * 32 + j * 16]);
-#pragma unroll
-      for (int n4 = 0; n4 < 4; ++n4)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          b[n4][j] = *reinterpret_cast<const v8bf*>(&sB[buf][(wn * 64 + n4 * 16 + fr) * T2_LDS + kg * 32 + j * 16]);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int n4 = 0; n4 < 4; ++n4) {
-          v4f p = {0.f, 0.f, 0.f, 0.f};
-          p = mfma_bf16_k32(a[mt][0], b[n4][0], p);
-          p = mfma_bf16_k32(a[mt][1], b[n4][1], p);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][n4][r] += p[r] * s;
+        for (int j = 0; j < 2; ++j) {
+          const v4i raw = *reinterpret_cast<const v4i*>(st + q2_bfrag(wn * 2 + j, u) + lane * 16);
+          bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
+          bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
         }
-      if (kk + 1 < T2_NK) lstore(buf ^ 1);
-      __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          v8bf af[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            af[i] = *reinterpret_cast<const v8bf*>(st + q2_afrag(wm * 2 + i, u, t) + lane * 16);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) p[i][j] = mfma_bf16_32x32x16(af[i], bf[j][t], p[i][j]);
+        }
+      }
+      if (s & 1) {  // end of a 128-wide K block: scale and fold
+        const float sc = swp[s >> 1];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += p[i][j][r] * sc;
+            p[i][j] = v16f{};
+          }
+      }
     }
+    // epilogue: weight by the pair's routing weight, one fp32 row per pair
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + mt * 16 + 4 * kg + r;
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
         if (row < cnt) {
           const float w = perm_w[seg + row];
-          float* dst = partial + (size_t)(seg + row) * H + nt * T2_BN + wn * 64 + fr;
+          float* dst = partial + (size_t)(seg + row) * H + nt * Q2_BN + wn * 64 + lr;
 #pragma unroll
-          for (int n4 = 0; n4 < 4; ++n4) dst[n4 * 16] = acc[mt][n4][r] * w;
+          for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
         }
       }
+    // No barrier needed before the next item: its prologue fills slots 0-2,
+    // which every wave finished reading before the last stage's barrier.
   }
 }
 
@@ -684,7 +710,15 @@ hipError_t launch_gemm1_tiled(const uint8_t* hidden, const float* hscale, int T,
 
 hipError_t launch_gemm2_tiled(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
                               const float* perm_w, float* partial, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm2_tiled_kernel, dim3(grid), dim3(256), 0, stream, c_act, w2, s2, hdr, perm_w, partial);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_tiled_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q2_NSTAGE * Q2_STAGE);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(gemm2_tiled_kernel, dim3(grid), dim3(64 * Q2_WAVES), Q2_NSTAGE * Q2_STAGE, stream, c_act, w2, s2,
+                     hdr, perm_w, partial);
   return hipGetLastError();
 }
 
