@@ -184,6 +184,34 @@ def cpu_baseline(sweep_names):
     }
 
 
+COPY_BYTES = 1 << 30  # calibration kernel: reads and writes 1 GiB (4x the MALL)
+
+
+def traffic_pass(dev, weights_gpu, sweep, reps):
+    """Launches for the HBM-traffic counters. The elementwise negation of a 1 GiB fp32
+    buffer into another (kernel name contains "neg") reads and writes exactly
+    COPY_BYTES each, so FETCH_SIZE and WRITE_SIZE of that launch give the scale from
+    counter KiB to bytes; then `reps` operator calls at each T of the sweep, so each
+    T contributes the same number of gemm1_decode_kernel launches."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    log(f"copy calibration done ({COPY_BYTES} B read + written per launch)")
+    cases = [Case(n, dev, weights_gpu) for n in sweep]
+    runner = Runner(dev, max(c.T for c in cases))
+    for c in cases:
+        for _ in range(reps):
+            runner.call(c)
+        torch.cuda.synchronize()
+        log(f"T={c.T}: {reps} calls done")
+    print(json.dumps({"traffic_pass": True, "copy_bytes": COPY_BYTES, "sweep_T": [c.T for c in cases],
+                      "calls_per_T": reps, "gemm1_algorithmic_bytes_mean":
+                      round(statistics.fmean(c.gemm1_bytes for c in cases))}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,6 +220,9 @@ def main():
     ap.add_argument("--reps", type=int, default=30, help="event-timed calls per T for per-kernel figures")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill/skew summary")
+    ap.add_argument("--traffic-pass", action="store_true",
+                    help="only run the launches a rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE pass reads: a copy "
+                         "kernel of known size, then --reps operator calls at each T of the sweep")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -208,6 +239,9 @@ def main():
     weights_cpu = wl.make_weights()
     weights_gpu = [t.to(dev) for t in weights_cpu]
     sweep = list(wl.DECODE_SWEEP)
+    if args.traffic_pass:
+        traffic_pass(dev, weights_gpu, sweep, args.reps)
+        return
     extra = [] if args.no_extra else ["t16", "prefill_t1024", "prefill_t8192", "skew_t4096"]
     cases = {n: Case(n, dev, weights_gpu) for n in sweep + extra}
     runner = Runner(dev, max(c.T for c in cases.values()))

@@ -10,18 +10,21 @@
 // GEMM1 runs on the e4m3 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
 // scales). One MFMA covers exactly one 128-wide K block, so the fp32 block
 // scales are applied once per block: acc += P * (s_act[row, kb] * s_w[nb, kb]).
-// GEMM2 runs on the bf16 MFMA (16x16x32): e4m3 weights widen to bf16 exactly;
-// the bf16 C keeps the SwiGLU output to 8 significant bits.
+// GEMM2 runs on the bf16 MFMA: e4m3 weights widen to bf16 exactly; the bf16 C
+// keeps the SwiGLU output to 8 significant bits.
 //
 // Two shapes of each GEMM:
-//   *_decode  -- few rows per expert. Persistent workgroups walk (active expert,
-//                column tile) items; the waves split K and preload their whole
-//                weight slice into registers, so each weight byte is read once
-//                and all loads are in flight together. Partial sums meet in LDS.
+//   *_decode  -- T <= 64, few rows per expert, weight-streaming bound.
+//                Persistent workgroups walk (active expert, column tile) items;
+//                the waves split K, so each weight byte is read once, and the
+//                next item's weights are in flight while the current one
+//                computes. Partial sums meet in LDS; GEMM2 also does the combine.
 //   *_tiled   -- many rows per expert (prefill). Persistent workgroups walk a
-//                device-built list of (expert, row tile, column tile) items with
-//                double-buffered LDS tiles; consecutive items share the weight
-//                tile and are kept on one XCD so its L2 serves the repeats.
+//                device-built list of (expert, row tile, column tile) items;
+//                operands go global -> LDS with direct loads into a ring of
+//                stages, in the exact order the MFMA reads them. The workgroups
+//                of one XCD take consecutive items, which share the weight tile,
+//                so that XCD's L2 serves the repeats.
 #include "moe_common.h"
 #include "moe_small_dispatch.h"
 
