@@ -17,8 +17,9 @@ hipError_t launch_dispatch_small(const int32_t*, const float*, int, int, Dispatc
 hipError_t launch_gemm1_decode(const uint8_t*, const float*, int, int, const uint8_t*, const float*, const int32_t*,
                                const float*, DispatchHeader*, int32_t*, float*, int32_t*, uint16_t*, int,
                                hipStream_t);
-hipError_t launch_gemm2_combine_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*,
-                                       const float*, const int32_t*, int, uint16_t*, int, hipStream_t);
+hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
+                               float*, int, hipStream_t);
+int gemm2_decode_blocks_per_cu();
 int gemm1_decode_blocks_per_cu();
 hipError_t launch_gemm1_tiled(const uint8_t*, const float*, int, const uint8_t*, const float*,
                               const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
@@ -133,8 +134,8 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
 }
 
 // Stage 0: routing (+ dispatch in the prefill shape); 1: GEMM1 + SwiGLU (+ the
-// in-workgroup dispatch in the decode shape); 2: GEMM2 x weight (+ the ordered
-// combine in the decode shape); 3: the combine (prefill shape only).
+// in-workgroup dispatch in the decode shape); 2: GEMM2 x weight into one fp32
+// row per pair; 3: the ordered combine to bf16.
 hipError_t run_stage(int stage, const Call& c) {
   using namespace moe;
   const int max_active = c.T * TOP_K < E_LOCAL ? c.T * TOP_K : E_LOCAL;
@@ -156,13 +157,13 @@ hipError_t run_stage(int stage, const Call& c) {
       return launch_gemm1_tiled(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
                                 (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
-      if (c.decode)
-        return launch_gemm2_combine_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.tok_pair, c.T, c.out, H / 16,
-                                           c.stream);
+      if (c.decode) {
+        const int grid = std::min(max_active * (H / 32), cu_count() * gemm2_decode_blocks_per_cu());
+        return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, grid, c.stream);
+      }
       return launch_gemm2_tiled(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() + 7) / 8 * 8,
                                 c.stream);
     case 3:
-      if (c.decode) return hipSuccess;
       return launch_combine(c.partial, c.tok_pair, c.T, c.out, c.stream);
     default:
       return hipErrorInvalidValue;

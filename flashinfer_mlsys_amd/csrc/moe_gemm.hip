@@ -58,36 +58,75 @@ __device__ __forceinline__ float silu_mul(float x1, float x2) {
 // consecutive indices.
 __device__ __forceinline__ int xcd_remap(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
 
+// Direct global -> LDS loads: lane l's 16 (or 4) bytes land at lds_dst + 16 l (4 l);
+// lds_dst must be uniform over the wave. The compiler does not track these LDS
+// writes: readers wait with an explicit s_waitcnt vmcnt.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void lds_direct16(const void* gsrc, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_direct4(const void* gsrc, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 4, 0, 0);
+}
+// Barrier for LDS traffic only. __syncthreads() also orders global memory, and
+// since global stores count in vmcnt like loads, it waits for every load in
+// flight (here: prefetched weights) whenever a store precedes it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ v8i lds_frag(const uint8_t* f) {
+  const int lane = threadIdx.x & 63;
+  const v4i lo = *reinterpret_cast<const v4i*>(f + lane * 16);
+  const v4i hi = *reinterpret_cast<const v4i*>(f + 1024 + lane * 16);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // GEMM1 + SwiGLU, decode shape (T <= 64).
 //
-// Every workgroup first derives the dispatch from the routing output in its own
-// LDS (dispatch_small), so the weight stream starts without reading a header
-// back from memory; workgroup 0 also stores the dispatch for GEMM2.
+// Every workgroup derives the dispatch from the routing output in its own LDS
+// (dispatch_small_*): the per-expert counts first, then the first two items'
+// weights are requested, then the token lists, so the weight stream starts
+// before the lists exist and without reading a header back from memory.
+// Workgroup 0 also stores the dispatch for GEMM2.
+//
 // Items are (active expert, 8-column tile): the MFMA's 16 B columns are W13
 // rows n..n+7 (X1) in lanes 0-7 and 2048+n..2048+n+7 (X2) in lanes 8-15, so
 // one expert spreads over 256 items and column c's X1 and X2 meet in the LDS
 // reduction. Each of the 8 waves owns 7 of the 56 K blocks. A workgroup (one
 // per CU) takes a contiguous run of items, so consecutive items mostly share
-// the expert: an expert with at most 16 rows keeps its activation fragments in
-// registers across items and only the weights stream, double-buffered in
-// registers (item i+1's weights are in flight while item i computes).
+// the expert. Weights stream through a 3-deep register ring: items i+1 and i+2
+// are in flight while item i computes. The activation rows of the current
+// expert (16 per pass) sit in LDS in MFMA fragment order, each wave holding
+// only its own K slice (direct global -> LDS loads), so no barrier guards
+// them; the one barrier per pass is the cross-wave reduction, whose buffer
+// alternates between passes.
 // ---------------------------------------------------------------------------
 constexpr int D1_WAVES = 8;
 constexpr int D1_KPW = NB_H / D1_WAVES;  // 7 K blocks per wave
 constexpr int D1_NT = I / 8;             // items per expert
+constexpr int D1_LOADS = 2 * D1_KPW;     // 16 B loads per lane for one item's weights
 static_assert(NB_H % D1_WAVES == 0, "K slices");
 static_assert(64 * D1_WAVES >= SMALL_P, "dispatch_small needs 512 threads");
+static_assert(D1_LOADS == 14, "the vmcnt immediates below count 14 loads per item");
 
 struct G1Shared {
   SmallDispatch d;
-  float red[D1_WAVES][4][64];
-  __attribute__((aligned(16))) float sa[NB_H][SMALL_T];  // activation scales of the current expert's rows
+  float red[2][D1_WAVES][4][64];
+  __attribute__((aligned(16))) uint8_t a[D1_WAVES][D1_KPW][2][1024];  // wave's K slice, 16 rows, fragment halves
+  __attribute__((aligned(16))) float sa[D1_WAVES][D1_KPW][16];        // their activation scales
 };
 
 struct G1State {
   int cur_le = -1;
-  bool a_resident = false;  // a[] holds rows 0..15 of expert cur_le
+  bool a_resident = false;  // sh.a holds rows 0..15 of expert cur_le
+  int phase = 0;            // reductions done (selects the red buffer)
 };
 
 __device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __restrict__ w13, int le, int nt, int kb0) {
@@ -98,11 +137,42 @@ __device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __res
   for (int kk = 0; kk < D1_KPW; ++kk) b[kk] = load_v8i(wp + kk * BLK);
 }
 
-// One item (expert, 8-column tile) with its weights already requested into b;
-// requests the next item's weights into bn once this item's activation loads
-// are out (so waiting for those never waits for the prefetch).
-__device__ __forceinline__ void g1_item(int item, int next, v8i (&a)[D1_KPW], v8i (&b)[D1_KPW], v8i (&bn)[D1_KPW],
-                                        G1State& st, G1Shared& sh, const uint8_t* __restrict__ hidden,
+// This wave's K slice of rows m0..m0+15 of expert le (rows past cnt repeat the
+// last one) and their activation scales into LDS (only this wave reads them). Lane l's fragment bytes are
+// row l % 16, K 32 (l / 16) + [0, 32): half h holds bytes [16 h, 16 h + 16).
+__device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restrict__ hidden,
+                                           const float* __restrict__ hscale, int T, int le, int m0, int wave) {
+  const SmallDispatch& d = sh.d;
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int cnt = d.cnt[le], seg = d.seg[le], kb0 = wave * D1_KPW;
+  // scales by 4 B direct loads: entry i = 16 kk + r of the wave's block, lanes past 112 masked
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = lane + 64 * j;
+    if (i < D1_KPW * 16) {
+      const int kk = i >> 4, r = i & 15;
+      lds_direct4(hscale + (size_t)(kb0 + kk) * T + d.tok[seg + min(m0 + r, cnt - 1)],
+                  reinterpret_cast<uint8_t*>(&sh.sa[wave][0][0] + 64 * j));
+    }
+  }
+  // rows through registers (not direct loads: the compiler cannot tell which LDS
+  // bytes a direct load writes, so reads of sh.a would wait for every load in flight)
+  const uint8_t* ap = hidden + (size_t)d.tok[seg + min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = *reinterpret_cast<const v4i*>(ap + kk * BLK + 16 * h);
+}
+
+// One item with its weights in b (requested two items ago); requests item + 2
+// into b2 (always when PF, else if it exists). The steady-state loop uses PF so
+// that every path issues the same loads: the compiler's wait before the MFMAs
+// then lets the next two items' weights stay in flight (vmcnt(28)); with a
+// conditional request it has to assume none and waits for all of them.
+template <bool PF>
+__device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i (&b2)[D1_KPW], G1State& st,
+                                        G1Shared& sh, const uint8_t* __restrict__ hidden,
                                         const float* __restrict__ hscale, int T, const uint8_t* __restrict__ w13,
                                         const float* __restrict__ s13, uint16_t* __restrict__ c_act) {
   const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
@@ -111,60 +181,63 @@ __device__ __forceinline__ void g1_item(int item, int next, v8i (&a)[D1_KPW], v8
   const SmallDispatch& d = sh.d;
   const int le = __builtin_amdgcn_readfirstlane(d.active[item / D1_NT]), nt = item % D1_NT;
   const int cnt = __builtin_amdgcn_readfirstlane(d.cnt[le]), seg = __builtin_amdgcn_readfirstlane(d.seg[le]);
-  if (le != st.cur_le) {  // uniform over the workgroup
-    __syncthreads();
-    for (int i = tid; i < NB_H * cnt; i += blockDim.x) {
-      const int kb = i / cnt, r = i - kb * cnt;
-      sh.sa[kb][r] = hscale[(size_t)kb * T + d.tok[seg + r]];
-    }
-    __syncthreads();
-    st.cur_le = le;
-    st.a_resident = false;
+  const bool stage = !(st.a_resident && st.cur_le == le);  // uniform over the workgroup
+  if (stage) g1_stage_a(sh, hidden, hscale, T, le, 0, wave);
+  const int n2 = item + 2;
+  const bool pf = PF || n2 < end;
+  if (pf) g1_load_w(b2, w13, __builtin_amdgcn_readfirstlane(d.active[n2 / D1_NT]), n2 % D1_NT, kb0);
+  if (stage) {  // the scales' direct loads (and everything before them) have landed; b2 may fly
+    if (pf) asm volatile("s_waitcnt vmcnt(14)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  // weight scales: the X1 block row (lanes 0-7) or the X2 block row (lanes 8-15), scalar loads
+  // weight scales: the X1 block row (lanes 0-7) or the X2 block row (lanes 8-15).
+  // Both are read at wave-uniform addresses (scalar loads, counted by lgkmcnt):
+  // a per-lane vector load here would make the MFMAs wait for vmcnt(0), i.e.
+  // for the prefetched weights of the next two items as well.
   const float* su = s13 + ((size_t)le * NB_N1 + (nt * 8) / BLK) * NB_H + kb0;
   const float* sg = su + (size_t)NB_I * NB_H;
-  bool prefetched = false;
-  for (int m0 = 0; m0 < cnt; m0 += 16) {
-    if (!st.a_resident) {
-      const int tok = d.tok[seg + min(m0 + fr, cnt - 1)];
-      const uint8_t* ap = hidden + (size_t)tok * H + kb0 * BLK + kg * 32;
+  float swu[D1_KPW], swg[D1_KPW];
 #pragma unroll
-      for (int kk = 0; kk < D1_KPW; ++kk) a[kk] = load_v8i(ap + kk * BLK);
-      st.a_resident = cnt <= 16;
+  for (int kk = 0; kk < D1_KPW; ++kk) {
+    swu[kk] = su[kk];
+    swg[kk] = sg[kk];
+  }
+  for (int m0 = 0; m0 < cnt; m0 += 16) {
+    if (m0 > 0) {  // a later 16-row pass of a big expert: restage A, wait for everything
+      g1_stage_a(sh, hidden, hscale, T, le, m0, wave);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    if (!prefetched) {
-      if (next >= 0) g1_load_w(bn, w13, __builtin_amdgcn_readfirstlane(d.active[next / D1_NT]), next % D1_NT, kb0);
-      prefetched = true;
-    }
-    if (m0 > 0) g1_load_w(b, w13, le, nt, kb0);  // later 16-row passes of a big expert re-read the tile
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < D1_KPW; ++kk) {
-      const v4f p = mfma_fp8_k128(a[kk], b[kk]);
-      const float sw = fr < 8 ? su[kk] : sg[kk];
-      const v4f sa = *reinterpret_cast<const v4f*>(&sh.sa[kb0 + kk][m0 + 4 * kg]);
+      const v8i a = lds_frag(&sh.a[wave][kk][0][0]);
+      const v4f p = mfma_fp8_k128(a, b[kk]);
+      const float sw = fr < 8 ? swu[kk] : swg[kk];
+      const v4f sa = *reinterpret_cast<const v4f*>(&sh.sa[wave][kk][4 * kg]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] += p[r] * (sa[r] * sw);
     }
+    float(&red)[D1_WAVES][4][64] = sh.red[st.phase & 1];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sh.red[wave][r][lane] = acc[r];
-    __syncthreads();
+    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    lds_barrier();
     if (tid < 256) {
       const int r = tid >> 6, ln = tid & 63;
       if ((ln & 15) < 8) {
         float x1 = 0.f, x2 = 0.f;
 #pragma unroll
         for (int w = 0; w < D1_WAVES; ++w) {
-          x1 += sh.red[w][r][ln];
-          x2 += sh.red[w][r][ln + 8];
+          x1 += red[w][r][ln];
+          x2 += red[w][r][ln + 8];
         }
         const int row = m0 + 4 * (ln >> 4) + r;
         if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = f32_to_bf16_rne(silu_mul(x1, x2));
       }
     }
-    __syncthreads();
+    ++st.phase;
   }
+  st.cur_le = le;
+  st.a_resident = cnt <= 16;
 }
 
 __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
@@ -172,54 +245,162 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, const int32_t* __restrict__ topk_ids,
     const float* __restrict__ topk_w, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
     float* __restrict__ perm_w, int32_t* __restrict__ tok_pair, uint16_t* __restrict__ c_act) {
-  __shared__ G1Shared sh;
-  dispatch_small(topk_ids, topk_w, T, offset, sh.d);
-  if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
+  extern __shared__ __attribute__((aligned(16))) uint8_t g1d_lds[];
+  G1Shared& sh = *reinterpret_cast<G1Shared*>(g1d_lds);
+  dispatch_small_counts(topk_ids, topk_w, T, offset, sh.d);
   const int total = sh.d.nact * D1_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int begin = blockIdx.x * per, end = min(total, begin + per);
   const int kb0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * D1_KPW;
-  G1State st;
-  v8i a[D1_KPW], b0[D1_KPW], b1[D1_KPW];
-  if (begin < end) g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
-  for (int item = begin; item < end; item += 2) {
-    g1_item(item, item + 1 < end ? item + 1 : -1, a, b0, b1, st, sh, hidden, hscale, T, w13, s13, c_act);
-    if (item + 1 < end)
-      g1_item(item + 1, item + 2 < end ? item + 2 : -1, a, b1, b0, st, sh, hidden, hscale, T, w13, s13, c_act);
+  v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
+  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
+  if (ring) {
+    g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
+    g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
+  } else {
+    if (begin < end) g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
+    if (begin + 1 < end)
+      g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
   }
+  dispatch_small_lists(T, offset, sh.d);
+  if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
+  G1State st;
+  int item = begin;
+  if (ring) {
+    for (; item + 4 < end; item += 3) {  // items item+2..item+4 exist: unconditional requests
+      g1_item<true>(item, end, b0, b2, st, sh, hidden, hscale, T, w13, s13, c_act);
+      g1_item<true>(item + 1, end, b1, b0, st, sh, hidden, hscale, T, w13, s13, c_act);
+      g1_item<true>(item + 2, end, b2, b1, st, sh, hidden, hscale, T, w13, s13, c_act);
+    }
+  }
+  // the last (at most four) items; b0 holds item, b1 item + 1
+  if (item < end) g1_item<false>(item, end, b0, b2, st, sh, hidden, hscale, T, w13, s13, c_act);
+  if (item + 1 < end) g1_item<false>(item + 1, end, b1, b0, st, sh, hidden, hscale, T, w13, s13, c_act);
+  if (item + 2 < end) g1_item<false>(item + 2, end, b2, b1, st, sh, hidden, hscale, T, w13, s13, c_act);
+  if (item + 3 < end) g1_item<false>(item + 3, end, b0, b2, st, sh, hidden, hscale, T, w13, s13, c_act);
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2 x routing weight + ordered combine, decode shape (T <= 64).
+// GEMM2 x routing weight, decode shape (T <= 64): weighted fp32 partial rows,
+// summed per token by combine_kernel.
 //
-// One workgroup per 16-column tile of the output (448 tiles). Its work units
-// are (active expert, K half): each of the 8 waves takes units round-robin,
-// widens 8 K blocks of W2 (16 rows = the tile's columns) from e4m3 to bf16 and
-// runs the expert's rows through the bf16 MFMA. Each unit's 16 columns for each
-// of the expert's rows land in an LDS slab indexed by pair; then every token's
-// output is sum over its local experts in ascending id of (half0 + half1) * w,
-// rounded once to bf16 (zeros for tokens with no local expert). No partial
-// rows in memory and no separate combine kernel.
+// Same streaming structure as the decode GEMM1. Items are (active expert,
+// 32-column tile of the output): W2 rows n..n+31 as two MFMA column blocks of
+// the bf16 16x16x32 MFMA; each of the 8 waves owns 2 of the 16 K blocks. Lane
+// (fr, kg) reads 32 contiguous e4m3 bytes of a W2 row per K block and the same
+// 32 K values (bf16, 64 B) of its activation row, so step j of a block takes K
+// 32 kg + 8 j + [0, 8) in both operands. Weights stream through a 3-deep
+// register ring (items i+1 and i+2 in flight while item i computes); an
+// expert's activation slice (<= 16 rows) stays in the wave's own LDS region
+// across its items.
 // ---------------------------------------------------------------------------
 constexpr int D2_WAVES = 8;
-constexpr int D2_KPU = NB_I / 2;  // K blocks per unit (half of K)
+constexpr int D2_COLS = 32;
+constexpr int D2_NT = H / D2_COLS;       // 224 items per expert
+constexpr int D2_KPW = NB_I / D2_WAVES;  // 2 K blocks per wave
+constexpr int D2_LD = 2 * 2 * D2_KPW;    // 16 B weight loads per lane per item
+static_assert(NB_I % D2_WAVES == 0 && D2_COLS == 32, "tile shape");
 
 struct G2Shared {
   int cnt[E_LOCAL];
   int seg[E_LOCAL + 1];
   int active[E_LOCAL];
   int nact;
-  int pair[SMALL_P];
   float pw[SMALL_P];
-  float slab[SMALL_P][2][16];
+  float red[2][D2_WAVES][2][4][64];
+  __attribute__((aligned(16))) uint8_t a[D2_WAVES][D2_KPW][4][1024];  // wave's activation slice, 16 B per lane
 };
 
-__global__ __launch_bounds__(64 * D2_WAVES, 4) void gemm2_combine_decode_kernel(
+struct G2State {
+  int cur_le = -1;
+  bool a_resident = false;
+  int phase = 0;
+};
+
+__device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __restrict__ w2, int le, int nt, int kb0) {
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const uint8_t* wp = w2 + ((size_t)le * H + nt * D2_COLS + cb * 16 + fr) * I + kb0 * BLK + kg * 32;
+#pragma unroll
+    for (int kk = 0; kk < D2_KPW; ++kk) {
+      b[(cb * D2_KPW + kk) * 2] = *reinterpret_cast<const v4i*>(wp + kk * BLK);
+      b[(cb * D2_KPW + kk) * 2 + 1] = *reinterpret_cast<const v4i*>(wp + kk * BLK + 16);
+    }
+  }
+}
+
+template <bool PF>
+__device__ __forceinline__ void g2_item(int item, int end, v4i (&b)[D2_LD], v4i (&b2)[D2_LD], G2State& st, G2Shared& sh, const uint16_t* __restrict__ c_act,
+                                        const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+                                        float* __restrict__ partial) {
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kb0 = wave * D2_KPW;
+  const int le = __builtin_amdgcn_readfirstlane(sh.active[item / D2_NT]), nt = item % D2_NT;
+  const int cnt = __builtin_amdgcn_readfirstlane(sh.cnt[le]), seg = __builtin_amdgcn_readfirstlane(sh.seg[le]);
+  const bool stage = !(st.a_resident && st.cur_le == le);
+  const int n2 = item + 2;
+  const float* sp = s2 + ((size_t)le * NB_H + (nt * D2_COLS) / BLK) * NB_I + kb0;  // wave-uniform: scalar loads
+  float sw[D2_KPW];
+#pragma unroll
+  for (int kk = 0; kk < D2_KPW; ++kk) sw[kk] = sp[kk];
+  auto load_a = [&](int m0) {  // this wave's slice of rows m0..m0+15 into its own LDS region
+    const uint16_t* ap = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
+#pragma unroll
+    for (int kk = 0; kk < D2_KPW; ++kk)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<v4i*>(&sh.a[wave][kk][q][lane * 16]) = *reinterpret_cast<const v4i*>(ap + kk * BLK + 8 * q);
+  };
+  if (stage) load_a(0);
+  if (PF || n2 < end) g2_load_w(b2, w2, __builtin_amdgcn_readfirstlane(sh.active[n2 / D2_NT]), n2 % D2_NT, kb0);
+  for (int m0 = 0; m0 < cnt; m0 += 16) {
+    if (m0 > 0) load_a(m0);
+    v4f acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < D2_KPW; ++kk) {
+        v4f p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4i wq = b[(cb * D2_KPW + kk) * 2 + (j >> 1)];
+          const v8bf wb = fp8x8_to_bf16x8((uint32_t)wq[2 * (j & 1)], (uint32_t)wq[2 * (j & 1) + 1]);
+          p = mfma_bf16_k32(*reinterpret_cast<const v8bf*>(&sh.a[wave][kk][j][lane * 16]), wb, p);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[cb][r] += p[r] * sw[kk];
+      }
+    }
+    float(&red)[D2_WAVES][2][4][64] = sh.red[st.phase & 1];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][cb][r][lane] = acc[cb][r];
+    lds_barrier();
+    {
+      const int row = tid >> 5, col = tid & 31, cb = col >> 4, r = row & 3, src = (row >> 2) * 16 + (col & 15);
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < D2_WAVES; ++w) v += red[w][cb][r][src];
+      if (m0 + row < cnt) {
+        const int pr = seg + m0 + row;
+        partial[(size_t)pr * H + nt * D2_COLS + col] = v * sh.pw[pr];
+      }
+    }
+    ++st.phase;
+  }
+  st.cur_le = le;
+  st.a_resident = cnt <= 16;
+}
+
+__global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, const int32_t* __restrict__ tok_pair,
-    int T, uint16_t* __restrict__ out) {
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
   __shared__ G2Shared sh;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  const int tid = threadIdx.x;
   if (tid < E_LOCAL) {
     sh.cnt[tid] = hdr->counts[tid];
     sh.seg[tid] = hdr->seg_start[tid];
@@ -229,65 +410,40 @@ __global__ __launch_bounds__(64 * D2_WAVES, 4) void gemm2_combine_decode_kernel(
     sh.seg[E_LOCAL] = hdr->seg_start[E_LOCAL];
     sh.nact = hdr->n_active;
   }
-  if (tid < T * TOP_K) sh.pair[tid] = tok_pair[tid];
   __syncthreads();
+  const int total = sh.nact * D2_NT;
+  const int per = (total + gridDim.x - 1) / gridDim.x;
+  const int begin = blockIdx.x * per, end = min(total, begin + per);
+  const int kb0 = __builtin_amdgcn_readfirstlane(tid >> 6) * D2_KPW;
+  v4i b0[D2_LD], b1[D2_LD], b2[D2_LD];
+  G2State st;
+  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
+  if (ring) {
+    g2_load_w(b0, w2, __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]), begin % D2_NT, kb0);
+    g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
+  } else {
+    if (begin < end) g2_load_w(b0, w2, __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]), begin % D2_NT, kb0);
+    if (begin + 1 < end)
+      g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
+  }
   const int P = sh.seg[E_LOCAL];
   for (int p = tid; p < P; p += blockDim.x) sh.pw[p] = perm_w[p];
-  const int units = 2 * sh.nact;
-
-  for (int nt = blockIdx.x; nt < H / 16; nt += gridDim.x) {
-    for (int u = wave; u < units; u += D2_WAVES) {
-      const int le = sh.active[u >> 1], h = u & 1;
-      const int cnt = sh.cnt[le], seg = sh.seg[le];
-      const int kb0 = h * D2_KPU;
-      const uint8_t* wrow = w2 + ((size_t)le * H + nt * 16 + fr) * I + kb0 * BLK + kg * 32;
-      const float* sw = s2 + ((size_t)le * NB_H + (nt * 16) / BLK) * NB_I + kb0;
-      for (int m0 = 0; m0 < cnt; m0 += 16) {
-        const uint16_t* arow = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-        // two steps of 4 K blocks: activation rows (L2) first, then the weights
-#pragma unroll 1
-        for (int q = 0; q < D2_KPU; q += 4) {
-          v8bf a[4][4];
-          v8i raw[4];
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[kk][j] = *reinterpret_cast<const v8bf*>(arow + (q + kk) * BLK + 8 * j);
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) raw[kk] = load_v8i(wrow + (q + kk) * BLK);
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            v4f p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              p = mfma_bf16_k32(a[kk][j], fp8x8_to_bf16x8((uint32_t)raw[kk][2 * j], (uint32_t)raw[kk][2 * j + 1]), p);
-            const float s = sw[q + kk];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += p[r] * s;
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + 4 * kg + r;
-          if (row < cnt) sh.slab[seg + row][h][fr] = acc[r];
-        }
-      }
+  __syncthreads();
+  int item = begin;
+  if (ring) {
+    for (; item + 4 < end; item += 3) {  // items item+2..item+4 exist
+      g2_item<true>(item, end, b0, b2, st, sh, c_act, w2, s2, partial);
+      g2_item<true>(item + 1, end, b1, b0, st, sh, c_act, w2, s2, partial);
+      g2_item<true>(item + 2, end, b2, b1, st, sh, c_act, w2, s2, partial);
     }
-    __syncthreads();
-    for (int o = tid; o < T * 16; o += blockDim.x) {
-      const int t = o >> 4, c = o & 15;
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < TOP_K; ++j) {
-        const int p = sh.pair[t * TOP_K + j];
-        if (p >= 0) acc += (sh.slab[p][0][c] + sh.slab[p][1][c]) * sh.pw[p];
-      }
-      out[(size_t)t * H + nt * 16 + c] = f32_to_bf16_rne(acc);
-    }
-    __syncthreads();
   }
+  // the last (at most four) items; b0, b1 hold item, item + 1
+  if (item < end) g2_item<false>(item, end, b0, b2, st, sh, c_act, w2, s2, partial);
+  if (item + 1 < end) g2_item<false>(item + 1, end, b1, b0, st, sh, c_act, w2, s2, partial);
+  if (item + 2 < end) g2_item<false>(item + 2, end, b2, b1, st, sh, c_act, w2, s2, partial);
+  if (item + 3 < end) g2_item<false>(item + 3, end, b0, b2, st, sh, c_act, w2, s2, partial);
 }
+
 
 // ---------------------------------------------------------------------------
 // Shared item list for the tiled kernels: every workgroup rebuilds the
@@ -351,23 +507,6 @@ constexpr int Q1_STAGE = Q1_SCALE_OFF + Q1_BM * 4;
 constexpr int Q1_NSTAGE = 3;
 static_assert(2 * (Q1_AFR + Q1_BFR) % Q1_WAVES == 0, "even job split");
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ void lds_direct16(const void* gsrc, uint8_t* lds_dst) {
-  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 16, 0, 0);
-}
-__device__ __forceinline__ void lds_direct4(const void* gsrc, uint8_t* lds_dst) {
-  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 4, 0, 0);
-}
-__device__ __forceinline__ v8i lds_frag(const uint8_t* f) {
-  const int lane = threadIdx.x & 63;
-  const v4i lo = *reinterpret_cast<const v4i*>(f + lane * 16);
-  const v4i hi = *reinterpret_cast<const v4i*>(f + 1024 + lane * 16);
-  v8i r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return r;
-}
 
 __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
@@ -638,26 +777,25 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
                                                       const int32_t* __restrict__ tok_pair, int T,
                                                       uint16_t* __restrict__ out) {
-  const int t = blockIdx.x;
+  // workgroup (t, c): token t, columns 1024 c .. 1024 c + 1023, 4 per thread
+  const int t = blockIdx.x, h = blockIdx.y * 1024 + threadIdx.x * 4;
   int p[TOP_K];
 #pragma unroll
   for (int j = 0; j < TOP_K; ++j) p[j] = tok_pair[(size_t)t * TOP_K + j];
+  float4 v[TOP_K];
 #pragma unroll
-  for (int i = 0; i < H / 1024; ++i) {
-    const int h = i * 1024 + threadIdx.x * 4;
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < TOP_K; ++j)
+    v[j] = p[j] >= 0 ? *reinterpret_cast<const float4*>(partial + (size_t)p[j] * H + h) : float4{0.f, 0.f, 0.f, 0.f};
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < TOP_K; ++j) {
-      if (p[j] >= 0) {
-        const float4 v = *reinterpret_cast<const float4*>(partial + (size_t)p[j] * H + h);
-        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-      }
+  for (int j = 0; j < TOP_K; ++j)  // ascending slot = ascending expert id
+    if (p[j] >= 0) {
+      acc.x += v[j].x; acc.y += v[j].y; acc.z += v[j].z; acc.w += v[j].w;
     }
-    uint2 o;
-    o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-    o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-    *reinterpret_cast<uint2*>(out + (size_t)t * H + h) = o;
-  }
+  uint2 o;
+  o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+  o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+  *reinterpret_cast<uint2*>(out + (size_t)t * H + h) = o;
 }
 
 }  // namespace moe
@@ -667,11 +805,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 namespace moe {
 
+static hipError_t gemm1_decode_set_lds() {
+  static bool done = false;
+  if (done) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_decode_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(G1Shared));
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
 int gemm1_decode_blocks_per_cu() {
   static int cached = 0;
   if (cached > 0) return cached;
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm1_decode_kernel, 64 * D1_WAVES, 0) != hipSuccess || n < 1)
+  if (gemm1_decode_set_lds() != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm1_decode_kernel, 64 * D1_WAVES, sizeof(G1Shared)) !=
+          hipSuccess ||
+      n < 1)
     n = 1;
   cached = n;
   return n;
@@ -682,17 +832,27 @@ hipError_t launch_gemm1_decode(const uint8_t* hidden, const float* hscale, int T
                                int32_t* perm_tok, float* perm_w, int32_t* tok_pair, uint16_t* c_act, int grid,
                                hipStream_t stream) {
   if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), 0, stream, hidden, hscale, T, offset, w13,
-                     s13, topk_ids, topk_w, hdr, perm_tok, perm_w, tok_pair, c_act);
+  const hipError_t e = gemm1_decode_set_lds();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), sizeof(G1Shared), stream, hidden, hscale, T,
+                     offset, w13, s13, topk_ids, topk_w, hdr, perm_tok, perm_w, tok_pair, c_act);
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_combine_decode(const uint16_t* c_act, const uint8_t* w2, const float* s2,
-                                       const DispatchHeader* hdr, const float* perm_w, const int32_t* tok_pair, int T,
-                                       uint16_t* out, int grid, hipStream_t stream) {
-  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm2_combine_decode_kernel, dim3(grid), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr,
-                     perm_w, tok_pair, T, out);
+int gemm2_decode_blocks_per_cu() {
+  static int cached = 0;
+  if (cached > 0) return cached;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm2_decode_kernel, 64 * D2_WAVES, 0) != hipSuccess || n < 1)
+    n = 1;
+  cached = n;
+  return n;
+}
+
+hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
+                               const float* perm_w, float* partial, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(grid), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr, perm_w,
+                     partial);
   return hipGetLastError();
 }
 
@@ -727,7 +887,8 @@ hipError_t launch_gemm2_tiled(const uint16_t* c_act, const uint8_t* w2, const fl
 
 hipError_t launch_combine(const float* partial, const int32_t* tok_pair, int T, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, stream, partial, tok_pair, T, out);
+  static_assert(H % 1024 == 0, "combine chunks");
+  hipLaunchKernelGGL(combine_kernel, dim3(T, H / 1024), dim3(256), 0, stream, partial, tok_pair, T, out);
   return hipGetLastError();
 }
 

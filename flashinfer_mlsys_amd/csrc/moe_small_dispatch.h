@@ -30,10 +30,12 @@ struct SmallDispatch {
   uint32_t mask[SMALL_T];
 };
 
-// Called by every thread of the workgroup; blockDim.x must be a multiple of 64
-// and at least SMALL_P. T <= SMALL_T.
-__device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, const float* __restrict__ wts,
-                                               int T, int offset, SmallDispatch& d) {
+// Phase 1 (called by every thread of the workgroup; blockDim.x a multiple of 64
+// and at least SMALL_P; T <= SMALL_T): the routed ids and weights into LDS, one
+// local-expert mask per token, per-expert counts, segment starts and the active
+// list. Enough to know which weights the workgroup will stream.
+__device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
+                                                      int T, int offset, SmallDispatch& d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   if (tid < SMALL_T) d.mask[tid] = 0u;
   if (tid < T * TOP_K) {
@@ -64,6 +66,12 @@ __device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, 
     for (int e = nact; e < E_LOCAL; ++e) d.active[e] = -1;
   }
   __syncthreads();
+}
+
+// Phase 2: every expert's ascending token list, the pair weights and each
+// (token, slot)'s pair index.
+__device__ __forceinline__ void dispatch_small_lists(int T, int offset, SmallDispatch& d) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const unsigned long long lt = (1ull << lane) - 1ull;
   for (int le = wave; le < E_LOCAL; le += nw) {
     const bool has = lane < T && ((d.mask[lane] >> le) & 1u);
@@ -79,6 +87,12 @@ __device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, 
     }
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, const float* __restrict__ wts, int T,
+                                               int offset, SmallDispatch& d) {
+  dispatch_small_counts(ids, wts, T, offset, d);
+  dispatch_small_lists(T, offset, d);
 }
 
 // Writes the dispatch to memory in the layout of dispatch_kernel (header,
