@@ -69,6 +69,32 @@ __device__ __forceinline__ void lds_direct16(const void* gsrc, uint8_t* lds_dst)
 __device__ __forceinline__ void lds_direct4(const void* gsrc, uint8_t* lds_dst) {
   __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)lds_dst, 4, 0, 0);
 }
+// Swizzled 16 x 128 B e4m3 fragment (2 KB), written by two direct loads of 8
+// whole row lines each: load j, lane l holds row 8 j + l / 8, 16 B chunk
+// (l % 8) ^ (l / 8) ^ j, at 1024 j + 16 l. An MFMA lane m (row m % 16, K bytes
+// 32 (m / 16) .. +32 = chunks 2 (m / 16) and 2 (m / 16) + 1) reads its two
+// chunks at the offsets below; every 16-lane group of either read hits 16
+// distinct 16 B bank slots, so the reads are conflict-free, and each load
+// instruction fetches 8 complete 128 B lines (half-line loads reach about a
+// third of the per-CU load bandwidth).
+__device__ __forceinline__ int frag_sw_offset(int r, int c) {
+  const int j = r >> 3, rr = r & 7;
+  return j * 1024 + 16 * (8 * rr + (c ^ rr ^ j));
+}
+__device__ __forceinline__ void frag_sw_offsets(int lane, int& lo, int& hi) {
+  const int r = lane & 15, q = lane >> 4;
+  lo = frag_sw_offset(r, 2 * q);
+  hi = frag_sw_offset(r, 2 * q + 1);
+}
+__device__ __forceinline__ v8i lds_frag_sw(const uint8_t* f, int lo, int hi) {
+  const v4i a = *reinterpret_cast<const v4i*>(f + lo);
+  const v4i b = *reinterpret_cast<const v4i*>(f + hi);
+  v8i r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
 // Barrier for LDS traffic only. __syncthreads() also orders global memory, and
 // since global stores count in vmcnt like loads, it waits for every load in
 // flight (here: prefetched weights) whenever a store precedes it.
@@ -474,6 +500,24 @@ __device__ __forceinline__ void build_tile_map(const DispatchHeader* hdr, TileMa
   __syncthreads();
 }
 
+// Item order for the tiled kernels: blocks of 8 row tiles x 4 column tiles.
+// With xcd_remap the 32 workgroups of one XCD take one block per round (on a
+// 256-CU part), so the concurrently streamed K blocks of 8 activation tiles
+// and 4 weight tiles are shared in that XCD's L2 (8 + 4 distinct tiles instead
+// of 32 + 1 for a column-tile-major order). Blocks run row-block major, all
+// column blocks of a row block back to back. Row tiles past total_m are empty
+// items (the caller skips them).
+constexpr int TB_M = 8, TB_N = 4;
+__device__ __forceinline__ int tiled_items(int total_m, int nt_count) {
+  return (total_m + TB_M - 1) / TB_M * TB_M * nt_count;
+}
+__device__ __forceinline__ void tiled_item_coords(int item, int nt_count, int& mg, int& nt) {
+  const int blk = item / (TB_M * TB_N), i = item % (TB_M * TB_N);
+  const int nbk = nt_count / TB_N;
+  mg = (blk / nbk) * TB_M + i % TB_M;
+  nt = (blk % nbk) * TB_N + i / TB_M;
+}
+
 __device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
   int e = 0;
   while (m.mt_prefix[e + 1] <= mg) ++e;
@@ -487,11 +531,10 @@ __device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
 //
 // Operands go global -> LDS with the direct load (global_load_lds_dwordx4):
 // one wave instruction moves 64 lanes x 16 B and lane l's bytes land at
-// base + 16 l, so the LDS holds every 16 x 128 e4m3 fragment in the order the
-// MFMA reads it and each fragment read is a linear 1 KB ds_read_b128 (no bank
-// conflicts, no staging registers). Lane l of a fragment half h carries K
-// bytes h*64 + (l/16)*16 .. +16 of row l%16 (the same K order for A and B, so
-// the products pair up). The activation scales of the item's rows ride along.
+// base + 16 l, with no staging registers. Each instruction loads 8 whole
+// 128 B row lines of a K block; the 16 B chunks are XOR-swizzled per row so
+// that the MFMA fragment reads (lds_frag_sw) are conflict-free. The activation
+// scales of the item's rows ride along.
 // Three LDS stages: the loads for K block kb+2 are issued while kb computes.
 // ---------------------------------------------------------------------------
 constexpr int FRAG_BYTES = 2048;           // one 16 x 128 e4m3 fragment
@@ -520,10 +563,15 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
   const int wm = wave & 1, wn = wave >> 1;
   build_tile_map<Q1_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = total_m * Q1_NT;
+  const int total = tiled_items(total_m, Q1_NT);
+  int flo, fhi;
+  frag_sw_offsets(lane, flo, fhi);
+  static_assert(Q1_NT % TB_N == 0, "column blocks");
 
   for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
-    const int nt = item / total_m, mg = item % total_m;
+    int mg, nt;
+    tiled_item_coords(item, Q1_NT, mg, nt);
+    if (mg >= total_m) continue;  // uniform over the workgroup
     const int e = find_expert(map, mg);
     const int m0 = (mg - map.mt_prefix[e]) * Q1_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
@@ -531,21 +579,23 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
     if (tid < Q1_BM) sTok[tid] = perm_tok[seg + m0 + min(tid, valid - 1)];
     __syncthreads();
 
-    // This wave's load jobs: fragment halves j = wave*6 + i of the 48 per stage.
+    // This wave's load jobs: fragment f = job / 2, rows 8 (job % 2) .. +7 of it, for
+    // the jobs wave*6 .. wave*6+5 of the 48 per stage. Each job reads 8 whole
+    // 128 B row lines of the K block (lane l: row l / 8, chunk (l % 8) ^ swizzle).
     const uint8_t* src[Q1_JOBS];
     int dst[Q1_JOBS];
 #pragma unroll
     for (int i = 0; i < Q1_JOBS; ++i) {
-      const int j = wave * Q1_JOBS + i, f = j >> 1, h = j & 1;
-      const int koff = h * 64 + kg * 16;
+      const int job = wave * Q1_JOBS + i, f = job >> 1, jj = job & 1;
+      const int rr = lane >> 3, koff = (((lane & 7) ^ rr ^ jj)) * 16;
       if (f < Q1_AFR) {
-        src[i] = hidden + (size_t)sTok[f * 16 + fr] * H + koff;
+        src[i] = hidden + (size_t)sTok[f * 16 + 8 * jj + rr] * H + koff;
       } else {
         const int g = f - Q1_AFR;
-        const int row = g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 + fr : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16 + fr;
+        const int row = (g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16) + 8 * jj + rr;
         src[i] = w13 + ((size_t)e * N1 + row) * H + koff;
       }
-      dst[i] = f * FRAG_BYTES + h * 1024;
+      dst[i] = f * FRAG_BYTES + jj * 1024;
     }
     const float* ssrc = hscale + sTok[wave * 16 + (lane & 15)];
     const float* su = s13 + ((size_t)e * NB_N1 + nt) * NB_H;          // X1 block row nt
@@ -564,6 +614,30 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
 
+    // Waves 4-7 apply block kb's scales one iteration late (before their own
+    // MFMAs of kb+1). Each SIMD runs one wave of each half, so after the
+    // barrier one wave reads fragments and issues MFMAs while the other does
+    // VALU work, instead of both doing the same phase at once.
+    const bool late = wave >= Q1_WAVES / 2;
+    v4f pu[4][2], pg[4][2];
+    v4f sa_k[4];
+    float swu_k = 0.f, swg_k = 0.f;
+    auto scale_phase = [&]() {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        v4f fu, fg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { fu[r] = sa_k[mt][r] * swu_k; fg[r] = sa_k[mt][r] * swg_k; }
+#pragma unroll
+        for (int n2 = 0; n2 < 2; ++n2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
+            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
+          }
+      }
+    };
+
     issue(0);
     issue(1);
 #pragma unroll 1
@@ -574,40 +648,32 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
       __builtin_amdgcn_s_barrier();  // every wave's loads for kb landed; kb-1 is fully read
       asm volatile("" ::: "memory");
       if (kb + 2 < NB_H) issue(kb + 2);
+      if (late && kb > 0) scale_phase();  // block kb-1
       const uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
-      const float swu = su[kb], swg = sg[kb];
-      // MFMA phase: all 16 products of this K block into their own registers ...
+      // MFMA phase: all 16 products of this K block into their own registers
       v8i a[4];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag(st + (wm * 4 + mt) * FRAG_BYTES);
-      v4f pu[4][2], pg[4][2];
+      for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag_sw(st + (wm * 4 + mt) * FRAG_BYTES, flo, fhi);
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) {
-        const v8i bu = lds_frag(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES);
-        const v8i bg = lds_frag(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES);
+        const v8i bu = lds_frag_sw(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
+        const v8i bg = lds_frag_sw(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
           pu[mt][n2] = mfma_fp8_k128(a[mt], bu);
           pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
         }
       }
-      // ... then the fp32 block-scale FMAs (overlap the other wave's MFMA phase).
+      // this block's scales (read now: the slot is refilled after the next barrier)
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
-        v4f fu, fg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
-#pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
-            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
-          }
-      }
+      for (int mt = 0; mt < 4; ++mt)
+        sa_k[mt] = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
+      swu_k = su[kb];
+      swg_k = sg[kb];
+      if (!late) scale_phase();
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
     }
+    if (late) scale_phase();  // block 55
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -672,10 +738,13 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
   const int lr = lane & 31, lg = lane >> 5;
   build_tile_map<Q2_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = total_m * Q2_NT;
+  const int total = tiled_items(total_m, Q2_NT);
+  static_assert(Q2_NT % TB_N == 0, "column blocks");
 
   for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
-    const int nt = item / total_m, mg = item % total_m;
+    int mg, nt;
+    tiled_item_coords(item, Q2_NT, mg, nt);
+    if (mg >= total_m) continue;  // uniform over the workgroup
     const int e = find_expert(map, mg);
     const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
