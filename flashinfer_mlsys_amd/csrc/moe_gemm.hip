@@ -696,27 +696,29 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
 // form runs at well under half of it), 8 waves as 2 (rows) x 4 (columns), each
 // 64 x 64 = 2 x 2 tiles of 32 x 32.
 //
-// Both operands arrive by direct global -> LDS loads into a 4-slot ring, three
-// 64-wide K stages ahead of the MFMAs, so no load waits in registers. In LDS a
-// W2 block (32 rows x 32 K, e4m3) holds in lane l's 16 B row l % 32, K
-// 16 (l / 32) + [0, 16); each lane reads its 16 B linearly and widens them
-// exactly to bf16 as two MFMA steps: step t takes K 16 g + 8 t + [0, 8) in lane
-// group g = l / 32. The activation fragments (bf16 SwiGLU output) are loaded
-// in that same K order, which the MFMA sum does not see. The fp32 weight-block
-// scale is applied once per 128-wide K block.
+// One stage is one 128-wide K block (the W2 scale block): the activation tile
+// (128 rows x 256 B bf16) and the W2 tile (256 rows x 128 B e4m3), 64 KB, in a
+// 2-slot LDS ring; the next block's direct loads fly while this one computes.
+// Every load instruction moves 8 whole 128 B row lines, and the LDS holds
+// 32-row x 128 B regions with the 16 B chunks XOR-swizzled per row (sw32), so
+// the fragment reads are conflict-free. K order inside a block (any bijection
+// shared by both operands leaves the MFMA sums unchanged): MFMA step t, lane
+// group g takes K 16 (2 (t / 2) + g) + 8 (t % 2) + [0, 8). A lane therefore
+// reads one 16 B W2 chunk per pair of steps and widens it exactly to bf16,
+// and reads the matching 16 B of bf16 activations per step. The fp32 weight
+// block scale is applied once per block.
 // ---------------------------------------------------------------------------
 constexpr int Q2_BM = 128;
 constexpr int Q2_BN = 256;
 constexpr int Q2_WAVES = 8;
-constexpr int Q2_NT = H / Q2_BN;      // 28 column tiles
-constexpr int Q2_KS = 64;             // K per stage
-constexpr int Q2_NS = I / Q2_KS;      // 32 stages
-constexpr int Q2_FRAG = 1024;         // 64 lanes x 16 B
-constexpr int Q2_A_BYTES = Q2_BM * Q2_KS * 2;  // 16 KB: 4 row blocks x 2 spans x 2 steps
-constexpr int Q2_B_BYTES = Q2_BN * Q2_KS;      // 16 KB: 8 row blocks x 2 spans
+constexpr int Q2_NT = H / Q2_BN;          // 28 column tiles
+constexpr int Q2_REG = 4096;              // 32 rows x 128 B
+constexpr int Q2_A_BYTES = Q2_BM * BLK * 2;  // 32 KB: 4 row blocks x 2 lines
+constexpr int Q2_B_BYTES = Q2_BN * BLK;      // 32 KB: 8 row blocks
 constexpr int Q2_STAGE = Q2_A_BYTES + Q2_B_BYTES;
-constexpr int Q2_NSTAGE = 4;
-static_assert(Q2_NS % Q2_NSTAGE == 0, "the last stage's slot must not be one the next item's prologue fills");
+constexpr int Q2_NSTAGE = 2;
+constexpr int Q2_JOBS = (Q2_A_BYTES + Q2_B_BYTES) / 1024 / Q2_WAVES;  // 8 load instructions per wave per block
+static_assert(Q2_JOBS == 8, "load jobs");
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -724,8 +726,13 @@ __device__ __forceinline__ v16f mfma_bf16_32x32x16(const v8bf& a, const v8bf& b,
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ int q2_afrag(int blk, int span, int t) { return ((blk * 2 + span) * 2 + t) * Q2_FRAG; }
-__device__ __forceinline__ int q2_bfrag(int blk, int span) { return Q2_A_BYTES + (blk * 2 + span) * Q2_FRAG; }
+// Offset of row r (0..31), 16 B chunk c (0..7) in a 32-row x 128 B region
+// written by 4 direct loads (load j: rows 8 j..8 j+7, lane l: row 8 j + l / 8,
+// chunk (l % 8) ^ (l / 8) ^ (j % 2), at 1024 j + 16 l).
+__device__ __forceinline__ int sw32(int r, int c) {
+  const int j = r >> 3, rr = r & 7;
+  return j * 1024 + 16 * (8 * rr + (c ^ rr ^ (j & 1)));
+}
 
 __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
@@ -741,6 +748,18 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
   const int total = tiled_items(total_m, Q2_NT);
   static_assert(Q2_NT % TB_N == 0, "column blocks");
 
+  // fragment read offsets: W2 chunk 2 p + g for step pair p; activation chunk
+  // 4 (p % 2) + 2 g + (t % 2) of line p / 2 for step t = 2 p + t % 2
+  int boff[4], aoff[2][2];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) boff[p] = sw32(lr, 2 * p + lg);
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) aoff[ph][tt] = sw32(lr, 4 * ph + 2 * lg + tt);
+  // this lane's place in a load instruction
+  const int ld_row = lane >> 3;
+
   for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
     int mg, nt;
     tiled_item_coords(item, Q2_NT, mg, nt);
@@ -749,77 +768,89 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
     const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
 
-    // Per stage each wave issues 2 activation loads (row block wave / 2, span
-    // wave & 1, steps 0 and 1) and 2 weight loads (row block wave, spans 0, 1).
-    const int ablk = wave >> 1, aspan = wave & 1;
-    const int arow = seg + min(m0 + ablk * 32 + lr, cnt - 1);
-    const uint8_t* asrc = reinterpret_cast<const uint8_t*>(c_act + (size_t)arow * I + aspan * 32 + lg * 16);
-    const uint8_t* bsrc = w2 + ((size_t)e * H + nt * Q2_BN + wave * 32 + lr) * I + lg * 16;
+    // Load jobs wave*8 .. wave*8+7: jobs 0-31 activations (row block jb / 8,
+    // line (jb / 4) % 2, rows 8 (jb % 4) ..), jobs 32-63 W2 (row block jb / 4,
+    // rows 8 (jb % 4) ..).
+    const uint8_t* src[Q2_JOBS];
+    int dst[Q2_JOBS];
+#pragma unroll
+    for (int i = 0; i < Q2_JOBS; ++i) {
+      const int job = wave * Q2_JOBS + i;
+      if (job < 32) {
+        const int ib = job >> 3, h = (job >> 2) & 1, rg = job & 3;
+        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
+        const int row = seg + min(m0 + ib * 32 + rg * 8 + ld_row, cnt - 1);
+        src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)row * I) + h * 128 + chunk * 16;
+        dst[i] = (ib * 2 + h) * Q2_REG + rg * 1024;
+      } else {
+        const int jb = (job - 32) >> 2, rg = job & 3;
+        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
+        src[i] = w2 + ((size_t)e * H + nt * Q2_BN + jb * 32 + rg * 8 + ld_row) * I + chunk * 16;
+        dst[i] = Q2_A_BYTES + jb * Q2_REG + rg * 1024;
+      }
+    }
     const float* swp = s2 + ((size_t)e * NB_H + (nt * Q2_BN + wn * 64) / BLK) * NB_I;
 
-    auto issue = [&](int s) {
-      uint8_t* st = q2_lds + (s % Q2_NSTAGE) * Q2_STAGE;
-      const uint8_t* as = asrc + s * Q2_KS * 2;
-      lds_direct16(as, st + q2_afrag(ablk, aspan, 0));
-      lds_direct16(as + 16, st + q2_afrag(ablk, aspan, 1));
-      const uint8_t* bs = bsrc + s * Q2_KS;
-      lds_direct16(bs, st + q2_bfrag(wave, 0));
-      lds_direct16(bs + 32, st + q2_bfrag(wave, 1));
+    auto issue = [&](int kb) {
+      uint8_t* st = q2_lds + (kb % Q2_NSTAGE) * Q2_STAGE;
+#pragma unroll
+      for (int i = 0; i < Q2_JOBS; ++i) {
+        // activation rows advance 256 B per K block, W2 rows 128 B
+        const int step = (wave * Q2_JOBS + i) < 32 ? 2 * BLK : BLK;
+        lds_direct16(src[i] + (size_t)kb * step, st + dst[i]);
+      }
     };
 
-    v16f acc[2][2], p[2][2];
+    v16f acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) { acc[i][j] = v16f{}; p[i][j] = v16f{}; }
+      for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
     issue(0);
-    issue(1);
-    issue(2);
 #pragma unroll 1
-    for (int s = 0; s < Q2_NS; ++s) {
-      // stage s has landed for this wave (stages s+1, s+2 may still fly) ...
-      if (s + 2 < Q2_NS) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else if (s + 1 < Q2_NS) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      // ... and for every wave; every wave is also done reading stage s-1's slot
-      __builtin_amdgcn_s_barrier();
+    for (int kb = 0; kb < NB_I; ++kb) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for block kb
+      __builtin_amdgcn_s_barrier();  // everyone's block kb landed; block kb-1 fully read
       asm volatile("" ::: "memory");
-      if (s + 3 < Q2_NS) issue(s + 3);
-
-      const uint8_t* st = q2_lds + (s % Q2_NSTAGE) * Q2_STAGE;
+      if (kb + 1 < NB_I) issue(kb + 1);
+      const uint8_t* st = q2_lds + (kb % Q2_NSTAGE) * Q2_STAGE;
+      const uint8_t* sa = st + (wm * 2) * 2 * Q2_REG;           // this wave's two activation row blocks
+      const uint8_t* sb = st + Q2_A_BYTES + (wn * 2) * Q2_REG;  // its two W2 row blocks
+      v16f pacc[2][2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) pacc[i][j] = v16f{};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
         v8bf bf[2][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const v4i raw = *reinterpret_cast<const v4i*>(st + q2_bfrag(wn * 2 + j, u) + lane * 16);
+          const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[p]);
           bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
           bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int tt = 0; tt < 2; ++tt) {
           v8bf af[2];
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const v8bf*>(st + q2_afrag(wm * 2 + i, u, t) + lane * 16);
+            af[i] = *reinterpret_cast<const v8bf*>(sa + (i * 2 + (p >> 1)) * Q2_REG + aoff[p & 1][tt]);
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) p[i][j] = mfma_bf16_32x32x16(af[i], bf[j][t], p[i][j]);
+            for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_bf16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
         }
       }
-      if (s & 1) {  // end of a 128-wide K block: scale and fold
-        const float sc = swp[s >> 1];
+      const float sc = swp[kb];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += p[i][j][r] * sc;
-            p[i][j] = v16f{};
-          }
-      }
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += pacc[i][j][r] * sc;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
     }
     // epilogue: weight by the pair's routing weight, one fp32 row per pair
 #pragma unroll
@@ -834,8 +865,7 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
           for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
         }
       }
-    // No barrier needed before the next item: its prologue fills slots 0-2,
-    // which every wave finished reading before the last stage's barrier.
+    __syncthreads();  // the next item's first loads refill the slot of this item's last block
   }
 }
 
