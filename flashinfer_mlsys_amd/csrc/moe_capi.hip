@@ -14,9 +14,9 @@ hipError_t launch_dispatch(const int32_t*, const float*, int, int, DispatchHeade
                            hipStream_t);
 hipError_t launch_dispatch_small(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
                                  hipStream_t);
-hipError_t launch_gemm1_decode(const uint8_t*, const float*, int, int, const uint8_t*, const float*, const int32_t*,
-                               const float*, DispatchHeader*, int32_t*, float*, int32_t*, uint16_t*, int,
-                               hipStream_t);
+hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const uint8_t*, const float*, int, int,
+                               const uint8_t*, const float*, int32_t*, float*, DispatchHeader*, int32_t*, float*,
+                               int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
                                float*, int, hipStream_t);
 int gemm2_decode_blocks_per_cu();
@@ -31,7 +31,8 @@ hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStrea
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kDecodeMaxTokens = 64;  // decode shape (LDS dispatch, streaming GEMMs) up to this many tokens
+constexpr int kDecodeMaxTokens = 64;        // decode shape (LDS dispatch, streaming GEMMs) up to this many tokens
+constexpr int kRouteInGemm1MaxTokens = 8;   // and routing inside GEMM1 (one token per wave) up to this many
 std::atomic<int> g_cu_count[kMaxDevices];
 std::atomic<int> g_path{0};
 thread_local const char* t_last_hip_error = "no error";
@@ -133,7 +134,8 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   return 1;  // valid, work to do
 }
 
-// Stage 0: routing (+ dispatch in the prefill shape); 1: GEMM1 + SwiGLU (+ the
+// Stage 0: routing (+ dispatch in the prefill shape; nothing for a decode call
+// of at most 8 tokens, routed inside GEMM1); 1: GEMM1 + SwiGLU (+ the
 // in-workgroup dispatch in the decode shape); 2: GEMM2 x weight into one fp32
 // row per pair; 3: the ordered combine to bf16.
 hipError_t run_stage(int stage, const Call& c) {
@@ -141,6 +143,7 @@ hipError_t run_stage(int stage, const Call& c) {
   const int max_active = c.T * TOP_K < E_LOCAL ? c.T * TOP_K : E_LOCAL;
   switch (stage) {
     case 0:
+      if (c.decode && c.T <= kRouteInGemm1MaxTokens) return hipSuccess;  // routed inside GEMM1
       if (c.decode) return launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, nullptr, c.stream);
       {
         hipError_t e = launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, c.tok_pair, c.stream);
@@ -151,8 +154,9 @@ hipError_t run_stage(int stage, const Call& c) {
     case 1:
       if (c.decode) {
         const int grid = std::min(max_active * (I / 8), cu_count() * gemm1_decode_blocks_per_cu());
-        return launch_gemm1_decode(c.hidden, c.hscale, c.T, c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr,
-                                   c.perm_tok, c.perm_w, c.tok_pair, c.c_act, grid, c.stream);
+        return launch_gemm1_decode(c.logits, c.bias, c.rsf, c.T <= kRouteInGemm1MaxTokens, c.hidden, c.hscale, c.T,
+                                   c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr, c.perm_tok, c.perm_w,
+                                   c.tok_pair, c.c_act, grid, c.stream);
       }
       return launch_gemm1_tiled(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
                                 (cu_count() + 7) / 8 * 8, c.stream);

@@ -26,6 +26,7 @@
 //                of one XCD take consecutive items, which share the weight tile,
 //                so that XCD's L2 serves the repeats.
 #include "moe_common.h"
+#include "moe_route_token.h"
 #include "moe_small_dispatch.h"
 
 namespace moe {
@@ -266,14 +267,30 @@ __device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i
   st.a_resident = cnt <= 16;
 }
 
+// With route_here (T <= D1_WAVES) the workgroup first routes the T tokens
+// itself, wave t token t, into its LDS (workgroup 0 also stores the ids and
+// weights), instead of reading the routing kernel's output: a small decode
+// call is then two launches, not three.
 __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
+    const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int route_here,
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T, int offset,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const int32_t* __restrict__ topk_ids,
-    const float* __restrict__ topk_w, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, int32_t* __restrict__ topk_ids,
+    float* __restrict__ topk_w, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
     float* __restrict__ perm_w, int32_t* __restrict__ tok_pair, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t g1d_lds[];
   G1Shared& sh = *reinterpret_cast<G1Shared*>(g1d_lds);
-  dispatch_small_counts(topk_ids, topk_w, T, offset, sh.d);
+  if (route_here) {
+    const int w = threadIdx.x >> 6;
+    if (w < T) route_token(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr);
+    __syncthreads();
+    if (blockIdx.x == 0 && (int)threadIdx.x < T * TOP_K) {
+      topk_ids[threadIdx.x] = sh.d.ids[threadIdx.x];
+      topk_w[threadIdx.x] = sh.d.wts[threadIdx.x];
+    }
+    dispatch_small_counts_lds(T, offset, sh.d);
+  } else {
+    dispatch_small_counts(topk_ids, topk_w, T, offset, sh.d);
+  }
   const int total = sh.d.nact * D1_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int begin = blockIdx.x * per, end = min(total, begin + per);
@@ -468,6 +485,7 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
   if (item + 1 < end) g2_item<false>(item + 1, end, b1, b0, st, sh, c_act, w2, s2, partial);
   if (item + 2 < end) g2_item<false>(item + 2, end, b2, b1, st, sh, c_act, w2, s2, partial);
   if (item + 3 < end) g2_item<false>(item + 3, end, b0, b2, st, sh, c_act, w2, s2, partial);
+
 }
 
 
@@ -926,15 +944,17 @@ int gemm1_decode_blocks_per_cu() {
   return n;
 }
 
-hipError_t launch_gemm1_decode(const uint8_t* hidden, const float* hscale, int T, int offset, const uint8_t* w13,
-                               const float* s13, const int32_t* topk_ids, const float* topk_w, DispatchHeader* hdr,
+hipError_t launch_gemm1_decode(const float* logits, const uint16_t* bias, float rsf, bool route_here,
+                               const uint8_t* hidden, const float* hscale, int T, int offset, const uint8_t* w13,
+                               const float* s13, int32_t* topk_ids, float* topk_w, DispatchHeader* hdr,
                                int32_t* perm_tok, float* perm_w, int32_t* tok_pair, uint16_t* c_act, int grid,
                                hipStream_t stream) {
-  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
+  if (T <= 0 || T > SMALL_T || (route_here && T > D1_WAVES)) return hipErrorInvalidValue;
   const hipError_t e = gemm1_decode_set_lds();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), sizeof(G1Shared), stream, hidden, hscale, T,
-                     offset, w13, s13, topk_ids, topk_w, hdr, perm_tok, perm_w, tok_pair, c_act);
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), sizeof(G1Shared), stream, logits, bias,
+                     rsf, route_here ? 1 : 0, hidden, hscale, T, offset, w13, s13, topk_ids, topk_w, hdr, perm_tok,
+                     perm_w, tok_pair, c_act);
   return hipGetLastError();
 }
 

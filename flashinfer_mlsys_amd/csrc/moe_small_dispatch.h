@@ -31,17 +31,13 @@ struct SmallDispatch {
 };
 
 // Phase 1 (called by every thread of the workgroup; blockDim.x a multiple of 64
-// and at least SMALL_P; T <= SMALL_T): the routed ids and weights into LDS, one
-// local-expert mask per token, per-expert counts, segment starts and the active
-// list. Enough to know which weights the workgroup will stream.
-__device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                      int T, int offset, SmallDispatch& d) {
+// and at least SMALL_P; T <= SMALL_T), from the routed ids and weights already
+// in d.ids / d.wts and visible to every thread: one local-expert mask per
+// token, per-expert counts, segment starts and the active list. Enough to know
+// which weights the workgroup will stream.
+__device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, SmallDispatch& d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   if (tid < SMALL_T) d.mask[tid] = 0u;
-  if (tid < T * TOP_K) {
-    d.ids[tid] = ids[tid];
-    d.wts[tid] = wts[tid];
-  }
   __syncthreads();
   if (tid < T * TOP_K) {
     const unsigned le = (unsigned)(d.ids[tid] - offset);
@@ -66,6 +62,18 @@ __device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict_
     for (int e = nact; e < E_LOCAL; ++e) d.active[e] = -1;
   }
   __syncthreads();
+}
+
+// Phase 1 from routed ids and weights in memory.
+__device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
+                                                      int T, int offset, SmallDispatch& d) {
+  const int tid = threadIdx.x;
+  if (tid < T * TOP_K) {
+    d.ids[tid] = ids[tid];
+    d.wts[tid] = wts[tid];
+  }
+  __syncthreads();
+  dispatch_small_counts_lds(T, offset, d);
 }
 
 // Phase 2: every expert's ascending token list, the pair weights and each
