@@ -28,7 +28,10 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   route_token(logits, bias, t, rsf, topk_ids, topk_w, tok_pair);
 }
 
-// One workgroup per local expert (grid = 32). See the file comment.
+// One workgroup per local expert (grid = 32): each walks all T tokens in
+// 256-token steps (two barriers per step), so its time grows with T; used
+// above DISPATCH_CHUNKED_MAX_T tokens, where dispatch_chunked_kernel's total
+// work (which grows with T^2) would be larger.
 __global__ __launch_bounds__(256) void dispatch_kernel(const int32_t* __restrict__ topk_ids,
                                                        const float* __restrict__ topk_w, int T, int offset,
                                                        DispatchHeader* __restrict__ hdr,
@@ -141,10 +144,106 @@ hipError_t launch_dispatch_small(const int32_t* topk_ids, const float* topk_w, i
   return hipGetLastError();
 }
 
+// One workgroup per 512-token chunk (grid = ceil(T / 512)), all chunks in
+// parallel and with no scratch memory: every workgroup histograms the local
+// ids of all T tokens (totals -> segment starts) and of the tokens before its
+// chunk (its offset inside each segment), then ranks its own tokens per expert
+// with one wave ballot per expert and a prefix over its 8 waves. Within each
+// expert the tokens stay in ascending order (reference ref_moe.py:131-145).
+// Workgroup 0 writes the header.
+constexpr int DISPATCH_CHUNK = 512;
+constexpr int DISPATCH_CHUNKED_MAX_T = 131072;
+
+__global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
+    const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,
+    int32_t* __restrict__ tok_pair) {
+  constexpr int NW = DISPATCH_CHUNK / 64;
+  __shared__ int hist_all[E_LOCAL], hist_pre[E_LOCAL], seg[E_LOCAL];
+  __shared__ unsigned long long wmask[NW][E_LOCAL];  // per wave and expert: lanes whose token selected it
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * DISPATCH_CHUNK;
+  if (tid < E_LOCAL) {
+    hist_all[tid] = 0;
+    hist_pre[tid] = 0;
+  }
+  __syncthreads();
+  for (int t = tid; t < T; t += DISPATCH_CHUNK) {
+    const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
+    const int4 a = row[0], b = row[1];
+    const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < TOP_K; ++j) {
+      const unsigned l = (unsigned)(v[j] - offset);
+      if (l < (unsigned)E_LOCAL) {
+        atomicAdd(&hist_all[l], 1);
+        if (t < t0) atomicAdd(&hist_pre[l], 1);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0, nact = 0;
+    for (int e = 0; e < E_LOCAL; ++e) {
+      seg[e] = acc;
+      if (blockIdx.x == 0) {
+        hdr->counts[e] = hist_all[e];
+        hdr->seg_start[e] = acc;
+        if (hist_all[e] > 0) hdr->active[nact++] = e;
+      }
+      acc += hist_all[e];
+    }
+    if (blockIdx.x == 0) {
+      hdr->seg_start[E_LOCAL] = acc;
+      hdr->n_active = nact;
+      for (int e = nact; e < E_LOCAL; ++e) hdr->active[e] = -1;
+    }
+  }
+  // this chunk's tokens: which local experts each selected, and in which slot
+  const int t = t0 + tid;
+  uint32_t mask = 0u;
+  int slot_of[TOP_K];
+  if (t < T) {
+    const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
+    const int4 a = row[0], b = row[1];
+    const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < TOP_K; ++j) {
+      slot_of[j] = v[j] - offset;
+      if ((unsigned)slot_of[j] < (unsigned)E_LOCAL) mask |= 1u << slot_of[j];
+    }
+  }
+  for (int e = 0; e < E_LOCAL; ++e) {  // uniform over the wave
+    const unsigned long long m = __ballot((mask >> e) & 1u);
+    if (lane == 0) wmask[wave][e] = m;
+  }
+  __syncthreads();
+  if (mask) {
+    const unsigned long long lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int j = 0; j < TOP_K; ++j) {
+      const int e = slot_of[j];
+      if ((unsigned)e >= (unsigned)E_LOCAL) continue;
+      int before = 0;  // earlier waves' tokens of this chunk that selected e
+      for (int w = 0; w < wave; ++w) before += __popcll(wmask[w][e]);
+      const int pos = seg[e] + hist_pre[e] + before + __popcll(wmask[wave][e] & lt);
+      perm_tok[pos] = t;
+      perm_w[pos] = topk_w[(size_t)t * TOP_K + j];
+      tok_pair[(size_t)t * TOP_K + j] = pos;
+    }
+  }
+}
+
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int offset, DispatchHeader* hdr,
                            int32_t* perm_tok, float* perm_w, int32_t* tok_pair, hipStream_t stream) {
-  hipLaunchKernelGGL(dispatch_kernel, dim3(E_LOCAL), dim3(256), 0, stream, topk_ids, topk_w, T, offset, hdr,
-                     perm_tok, perm_w, tok_pair);
+  if (T <= DISPATCH_CHUNKED_MAX_T) {
+    const int chunks = T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1;
+    hipLaunchKernelGGL(dispatch_chunked_kernel, dim3(chunks), dim3(DISPATCH_CHUNK), 0, stream, topk_ids, topk_w, T,
+                       offset, hdr, perm_tok, perm_w, tok_pair);
+  } else {
+    hipLaunchKernelGGL(dispatch_kernel, dim3(E_LOCAL), dim3(256), 0, stream, topk_ids, topk_w, T, offset, hdr,
+                       perm_tok, perm_w, tok_pair);
+  }
   return hipGetLastError();
 }
 

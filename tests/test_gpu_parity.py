@@ -119,6 +119,48 @@ def test_dispatch_bit_exact(case):
     _check_dispatch(case, ids, w, header, perm_tok, perm_w, pair)
 
 
+def _synthetic_ids(T, offset, seed):
+    """8 distinct ascending ids per token ((a + k s) mod 256 with s odd), plus
+    tokens with all 8 ids local and tokens with none."""
+    rng = np.random.default_rng(seed)
+    a = rng.integers(0, 256, T)
+    s = 2 * rng.integers(0, 128, T) + 1
+    ids = np.sort((a[:, None] + np.arange(8)[None, :] * s[:, None]) % 256, axis=1).astype(np.int32)
+    ids[::97] = offset + np.arange(8, dtype=np.int32) * 3          # all 8 local
+    far = (offset + 128) % 256
+    ids[5::89] = np.sort((far + np.arange(8, dtype=np.int32)) % 256)  # none local (the window is 32 wide)
+    w = rng.random((T, 8), dtype=np.float32)
+    return ids, w
+
+
+@pytest.mark.parametrize("T,offset", [(20000, 64), (140000, 0)])
+def test_dispatch_large_synthetic(dev, T, offset):
+    """Dispatch bit-exact at sizes past the benchmark's: many 512-token chunks
+    (T=20000) and the per-expert kernel used above 131072 tokens (T=140000),
+    against a numpy restatement of ref_moe.py:131-145."""
+    _say(f"dispatch synthetic T={T} offset={offset}")
+    ids, w = _synthetic_ids(T, offset, seed=T)
+    ids_d = torch.from_numpy(ids).to(dev)
+    w_d = torch.from_numpy(w).to(dev)
+    pair = torch.full((T, 8), -1, dtype=torch.int32, device=dev)
+    header, perm_tok, perm_w, pair = fm.dispatch(ids_d, w_d, pair, offset)
+    torch.cuda.synchronize()
+    h = header.cpu().numpy()
+    lists = [np.nonzero((ids == offset + e).any(axis=1))[0] for e in range(32)]
+    counts = np.array([len(x) for x in lists])
+    np.testing.assert_array_equal(h[:32], counts)
+    P = int(counts.sum())
+    assert h[32] == 0 and h[64] == P
+    np.testing.assert_array_equal(perm_tok.cpu().numpy()[:P], np.concatenate(lists))
+    pair_c, pw = pair.cpu().numpy(), perm_w.cpu().numpy()[:P]
+    local = (ids >= offset) & (ids < offset + 32)
+    assert ((pair_c >= 0) == local).all()
+    t_idx, j_idx = np.nonzero(local)
+    p_idx = pair_c[t_idx, j_idx]
+    np.testing.assert_array_equal(perm_tok.cpu().numpy()[p_idx], t_idx)
+    np.testing.assert_array_equal(pw[p_idx], w[t_idx, j_idx])
+
+
 @pytest.mark.parametrize("case", ALL, indirect=True)
 def test_route_dispatch_as_forward_runs_it(case):
     """Routing + dispatch exactly as the forward runs them (one fused kernel for T <= 64)."""
