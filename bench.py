@@ -344,6 +344,23 @@ def main():
         }
         log(f"{n}: {also[n]['us_per_call']} us/call, stages {[round(x, 1) for x in st]}")
 
+    # the producer-side activation quantiser (bf16 -> e4m3 + [56, T] scales), HBM-bound
+    if not args.no_extra:
+        qa = {}
+        for T in (64, 8192):
+            x = wl.hidden_bf16(T, 77).to(dev)
+            qbuf = (torch.empty((T, wl.H), dtype=torch.float8_e4m3fn, device=dev),
+                    torch.empty((wl.NB_H, T), dtype=torch.float32, device=dev))
+            g = runner.graph(lambda: fm.quantize_activations(x, out=qbuf), args.reps)
+            us = runner.graph_us(g, args.reps)
+            del g
+            nbytes = T * (wl.H * 2 + wl.H + wl.NB_H * 4)
+            qa[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
+                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+            log(f"quantize_activations T={T}: {us:.1f} us, {qa[f'T={T}']['GB_per_s']} GB/s")
+        also["quantize_activations"] = qa
+
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")

@@ -25,7 +25,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "workspace_size", "MoEInputError", "set_path"]
+__all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_activations", "workspace_size",
+           "MoEInputError", "set_path"]
 
 H = 7168
 I = 2048
@@ -168,6 +169,39 @@ def route(routing_logits, routing_bias, routed_scaling_factor):
                                          ids.data_ptr(), w.data_ptr(), pair.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_route")
     return ids, w, pair
+
+
+@torch.no_grad()
+def quantize_activations(hidden_bf16, out=None):
+    """Producer-side FP8 quantiser: bf16 [T, 7168] -> (hidden_states e4m3 [T, 7168],
+    hidden_states_scale fp32 [56, T]), the operator's own input format.
+
+    Per 1 x 128 block: scale = max(amax, 1e-12) / 448, q = e4m3(x / scale) with
+    round to nearest even (the reference's quantisation step,
+    solution/triton/dsl-temp1.py:479-484). ``out`` may pass preallocated
+    (q, scale) tensors.
+    """
+    _on_gpu(hidden_bf16, "hidden_bf16")
+    _req(hidden_bf16.dtype == torch.bfloat16 and hidden_bf16.dim() == 2 and hidden_bf16.shape[1] == H,
+         "hidden_bf16 must be bf16 [T, 7168]")
+    T = hidden_bf16.shape[0]
+    dev = hidden_bf16.device
+    if out is None:
+        q = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=dev)
+        scale = torch.empty((H // BLOCK, T), dtype=torch.float32, device=dev)
+    else:
+        q, scale = out
+        _req(q.dtype == torch.float8_e4m3fn and tuple(q.shape) == (T, H) and q.is_contiguous(),
+             "q must be a contiguous float8_e4m3fn [T, 7168]")
+        _req(scale.dtype == torch.float32 and tuple(scale.shape) == (H // BLOCK, T) and scale.is_contiguous(),
+             "scale must be a contiguous float32 [56, T]")
+    if T == 0:
+        return q, scale
+    x = _contig(hidden_bf16)
+    with torch.cuda.device(dev):
+        code = _lib.load().moe_fp8_quantize_activations(x.data_ptr(), T, q.data_ptr(), scale.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_quantize_activations")
+    return q, scale
 
 
 @torch.no_grad()

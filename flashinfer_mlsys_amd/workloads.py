@@ -148,6 +148,11 @@ def make_weights(seed: int = WEIGHT_SEED, threads: int = 16):
     return out
 
 
+def hidden_bf16(T: int, seed: int):
+    """The bf16 hidden states a workload's e4m3 hidden_states are quantised from."""
+    return _normal((seed, 12), (T, H), 1.0).to(torch.bfloat16)
+
+
 def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool = False):
     """(routing_logits fp32 [T,256], routing_bias bf16 [256], hidden e4m3 [T,H], hidden_scale [56,T])."""
     logits = _normal((seed, 10), (T, E_GLOBAL), 1.0)
@@ -157,7 +162,7 @@ def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool
             logits[:, g * 32:(g + 1) * 32] += 2.0
         logits[:, chosen] += 2.0
     bias = _normal((seed, 11), (E_GLOBAL,), 0.1).to(torch.bfloat16)
-    x = _normal((seed, 12), (T, H), 1.0).to(torch.bfloat16).to(torch.float32)
+    x = hidden_bf16(T, seed).to(torch.float32)
     hidden, hidden_scale = quantize_1x128(x) if T > 0 else (
         torch.empty((0, H), dtype=torch.float8_e4m3fn), torch.empty((NB_H, 0), dtype=torch.float32))
     return logits, bias, hidden, hidden_scale

@@ -121,6 +121,18 @@ int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_
                            float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
                            void* stream);
 
+/*
+ * Producer-side FP8 activation quantiser (the step before this operator:
+ * reference moe/weight_origins_dataflow.md:19-21, :131-142; its formula as in
+ * solution/triton/dsl-temp1.py:479-484). Per 1 x 128 block of the bf16 hidden
+ * states [T, 7168]: amax = max |x| clamped below at 1e-12, scale = amax / 448,
+ * q = e4m3(x / scale) with round to nearest even. Writes hidden_states e4m3
+ * [T, 7168] and hidden_states_scale fp32 [56, T] (transposed), i.e. exactly
+ * the operator's hidden_states / hidden_states_scale inputs. Stream-ordered.
+ */
+int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t* hidden_states,
+                                 float* hidden_states_scale, void* stream);
+
 /* Kernel shape used by moe_fp8_forward: 0 = by token count (default: the
  * decode shape for T <= 64, the prefill shape above), 1 = the same as 0
  * (the decode shape exists only for T <= 64), 2 = always the prefill shape.

@@ -49,6 +49,20 @@ def dequant_hidden(hidden_states, hidden_states_scale):
     return a * s_full
 
 
+def quantize_activations(x_bf16):
+    """Producer-side quantiser, the step before the operator: per 1x128 block of
+    bf16 hidden states, scale = max(amax, 1e-12) / 448 and q = e4m3(x / scale)
+    (torch's round-to-nearest-even cast), as solution/triton/dsl-temp1.py:479-484
+    quantises an activation. bf16 [T, 7168] -> (e4m3 [T, 7168], fp32 [56, T]).
+    The clamp to +-448 only guards the division's last-bit rounding (torch rounds
+    such values to 448 anyway)."""
+    T = x_bf16.shape[0]
+    xb = x_bf16.to(torch.float32).reshape(T, H // BLOCK, BLOCK)
+    scale = xb.abs().amax(dim=2).clamp(min=1e-12) / 448.0
+    q = (xb / scale.unsqueeze(2)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.reshape(T, H), scale.t().contiguous()
+
+
 def dequant_weight(w, s):
     """``ref_moe.py:80-92`` for one or more experts: W = fp8 * S[n/128, k/128] in fp32."""
     wf = w.to(torch.float32)

@@ -100,3 +100,22 @@ def rows_fp64(tokens, sel_ids, sel_w, hidden_codes, hidden_scale, w13_codes, s13
             c = x1 * (x2 / (1.0 + np.exp(-x2)))
             out[r] += float(sel_w[t, j]) * (w2 @ c)
     return out
+
+
+def e4m3_encode(x):
+    """float32 array -> OCP e4m3 codes (uint8), round to nearest, ties to the even
+    code, from the table of finite values (independent of torch's cast). Values
+    must lie in [-448, 448]; -0.0 encodes as 0x80."""
+    x = np.asarray(x, dtype=np.float32)
+    assert np.all(np.abs(x) <= 448.0)
+    table = e4m3_table()
+    pos_codes = np.arange(0x00, 0x7F)            # 0 .. 448, increasing values
+    pos_vals = table[pos_codes]
+    a = np.abs(x).astype(np.float64)
+    hi = np.clip(np.searchsorted(pos_vals, a, side="left"), 0, len(pos_vals) - 1)
+    lo = np.clip(hi - 1, 0, None)
+    d_hi = np.abs(pos_vals[hi] - a)
+    d_lo = np.abs(a - pos_vals[lo])
+    pick_lo = (d_lo < d_hi) | ((d_lo == d_hi) & (pos_codes[lo] % 2 == 0))
+    code = np.where(pick_lo, pos_codes[lo], pos_codes[hi]).astype(np.uint8)
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)

@@ -2,6 +2,7 @@ import os
 import sys
 
 import numpy as np
+import torch
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -51,3 +52,25 @@ def assert_close_bf16(actual_f32, expected_f32, what=""):
             f"{what}: {int(bad.sum())} of {bad.size} elements outside atol={ATOL} rtol={RTOL}; "
             f"first at {tuple(i)}: got {a[tuple(i)]!r} want {e[tuple(i)]!r}; "
             f"max abs err {np.abs(a - e).max():.4g}")
+
+from oracle import np_ref  # noqa: E402  (test infrastructure)
+
+
+def quant_edge_rows():
+    """bf16 rows whose blocks have closed-form quantisations: a power-of-two scale
+    (amax 448 * 2^-3) with every e4m3 value and every midpoint between two (ties);
+    an all-zero block; -0.0; bf16 subnormals; the largest bf16 values."""
+    vals = np_ref.e4m3_table()
+    fin = np.unique(vals[np.isfinite(vals) & (vals >= 0)])
+    mids = (fin[:-1] + fin[1:]) / 2
+    rows = np.zeros((3, 7168), dtype=np.float32)
+    scale = 2.0 ** -3
+    block = np.concatenate([[448.0], fin[:63], -mids[:64]])[:128] * scale  # exact in bf16
+    rows[0, :128] = block
+    rows[0, 128:256] = -block[::-1]
+    rows[1, 256:384] = np.float32(2.0 ** -130) * np.arange(1, 129, dtype=np.float32)  # bf16 subnormals
+    rows[1, 384] = -0.0
+    rows[2, 512:640] = np.linspace(-3.3e38, 3.3e38, 128, dtype=np.float32)
+    x = torch.from_numpy(rows).to(torch.bfloat16)
+    assert torch.equal(x[0, :128].float(), torch.from_numpy(block.astype(np.float32)))
+    return x

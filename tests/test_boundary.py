@@ -86,6 +86,16 @@ def test_route_and_dispatch_argument_errors(lib):
     assert lib.moe_fp8_dispatch(FAKE, FAKE, 4, 0, FAKE + 4, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_ALIGN
 
 
+def test_quantize_argument_errors(lib):
+    q = lib.moe_fp8_quantize_activations
+    assert q(FAKE, 0, FAKE, FAKE, None) == _lib.MOE_OK
+    assert q(FAKE, -1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert q(FAKE, (1 << 20) + 1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert q(None, 4, FAKE, FAKE, None) == _lib.MOE_ERR_NULL
+    assert q(FAKE, 4, FAKE, None, None) == _lib.MOE_ERR_NULL
+    assert q(FAKE, 4, FAKE + 8, FAKE, None) == _lib.MOE_ERR_ALIGN
+
+
 def test_set_path(lib):
     assert lib.moe_fp8_set_path(7) == -1
     old = lib.moe_fp8_set_path(2)

@@ -15,7 +15,7 @@ import flashinfer_mlsys_amd as fm
 from flashinfer_mlsys_amd import workloads as wl
 from oracle import cpu_ref
 
-from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden
+from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden, quant_edge_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -281,3 +281,33 @@ def test_graph_replay_matches_eager(case):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
+
+
+# --- producer-side activation quantiser ---------------------------------------
+
+@pytest.mark.parametrize("name", ["decode_t1", "t16", "decode_t64", "prefill_t1024", "prefill_t8192", "skew_t4096"])
+def test_quantize_activations_reproduces_reference_inputs(dev, name):
+    """The HIP quantiser turns a workload's bf16 hidden states into exactly the
+    e4m3 hidden_states / scales the reference was run on (sha256 in the fixture)."""
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    _say(f"quantize {name} T={w.T}")
+    q, s = fm.quantize_activations(wl.hidden_bf16(w.T, w.seed).to(dev))
+    torch.cuda.synchronize()
+    assert wl.fingerprint(q) == str(g["in_sha256"][2])
+    assert wl.fingerprint(s) == str(g["in_sha256"][3])
+
+
+def test_quantize_activations_edge_cases(dev):
+    """Bit-exact with the oracle on closed-form blocks (power-of-two scales with
+    every e4m3 value and every tie, zeros, -0.0, bf16 subnormals, the largest
+    bf16 values) and on a token count that is not a multiple of 16."""
+    gen = torch.Generator().manual_seed(9)
+    rnd = (torch.randn(37, 7168, generator=gen) * torch.logspace(-8, 8, 37).unsqueeze(1)).to(torch.bfloat16)
+    for x in (quant_edge_rows(), rnd):
+        q, s = fm.quantize_activations(x.to(dev))
+        torch.cuda.synchronize()
+        rq, rs = cpu_ref.quantize_activations(x)
+        np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), rq.view(torch.uint8).numpy())
+        np.testing.assert_array_equal(s.cpu().numpy(), rs.numpy())
+

@@ -11,7 +11,7 @@ import torch
 from flashinfer_mlsys_amd import workloads as wl
 from oracle import cpu_ref, np_ref
 
-from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden
+from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden, quant_edge_rows
 
 ALL = list(wl.WORKLOADS)
 
@@ -122,6 +122,49 @@ def test_oracle_rows_match_float64():
     np.testing.assert_allclose(out[tokens], ref, rtol=8e-3, atol=1e-4)
 
 
+# --- producer-side activation quantiser -------------------------------------
+
+@pytest.mark.parametrize("name", ALL)
+def test_quantize_reproduces_reference_inputs(name):
+    """On a workload's bf16 hidden states the quantiser restatement gives exactly
+    the e4m3 hidden_states and scales the reference was run on (their sha256 in
+    the golden fixture)."""
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    q, s = cpu_ref.quantize_activations(wl.hidden_bf16(w.T, w.seed))
+    assert wl.fingerprint(q) == str(g["in_sha256"][2])
+    assert wl.fingerprint(s) == str(g["in_sha256"][3])
+
+
+def test_quantize_closed_forms():
+    x = quant_edge_rows()
+    q, s = cpu_ref.quantize_activations(x)
+    codes = q.view(torch.uint8).numpy()
+    s = s.numpy()
+    # power-of-two scale: every code exact, ties to the even code
+    assert s[0, 0] == 2.0 ** -3 and s[1, 0] == 2.0 ** -3
+    want = np_ref.e4m3_encode((x[0, :128].float() / 2.0 ** -3).numpy())
+    np.testing.assert_array_equal(codes[0, :128], want)
+    assert codes[0, 0] == 0x7E                      # the block max is +448
+    assert codes[0, 255] == 0xFE                     # and its negation -448
+    # all-zero block: zeros with the floor scale
+    assert (codes[0, 256:384] == 0).all() and s[2, 0] == np.float32(1e-12) / np.float32(448.0)
+    # bf16 subnormals quantise like any other block; -0.0 keeps its sign
+    assert codes[1, 384] == 0x80
+    np.testing.assert_array_equal(
+        codes[1, 256:384], np_ref.e4m3_encode((x[1, 256:384].float() / float(s[2, 1])).clamp(-448, 448).numpy()))
+    # the largest bf16 values: scale = amax / 448 stays finite
+    assert np.isfinite(s[4, 2]) and codes[2, 639] == 0x7E and codes[2, 512] == 0xFE
+
+
+def test_quantize_matches_independent_encoder():
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn(8, cpu_ref.H, generator=gen) * torch.logspace(-6, 6, 8).unsqueeze(1)).to(torch.bfloat16)
+    q, s = cpu_ref.quantize_activations(x)
+    xs = (x.float().reshape(8, 56, 128) / s.t().reshape(8, 56, 1)).clamp(-448, 448).reshape(8, -1).numpy()
+    np.testing.assert_array_equal(q.view(torch.uint8).numpy(), np_ref.e4m3_encode(xs))
+
+
 # --- planted mistakes: each must make the checks above fail -----------------
 
 def _swapped_swiglu(A_e, W13_e, W2_e):
@@ -144,6 +187,20 @@ def _route_without_bias(logits, bias, rsf):
 
 
 _orig_route = cpu_ref.route
+
+
+def test_planted_quantiser_mistake_is_caught(monkeypatch):
+    """A quantiser that divides by the e4m3fnuz maximum (240) instead of 448 must
+    fail the reference-input check."""
+    def wrong(x_bf16):
+        T = x_bf16.shape[0]
+        xb = x_bf16.to(torch.float32).reshape(T, 56, 128)
+        scale = xb.abs().amax(dim=2).clamp(min=1e-12) / 240.0
+        q = (xb / scale.unsqueeze(2)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        return q.reshape(T, -1), scale.t().contiguous()
+    monkeypatch.setattr(cpu_ref, "quantize_activations", wrong)
+    with pytest.raises(AssertionError):
+        test_quantize_reproduces_reference_inputs("t16")
 
 
 @pytest.mark.parametrize("mutation", ["swiglu_halves", "block_scale_order", "bias_dropped"])
