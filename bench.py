@@ -319,7 +319,7 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("gemm1_decode_kernel", {}).get("hbm_bytes_per_launch")
     roofline = {
-        "kernel": "gemm1_decode_kernel (dispatch + GEMM1 + SwiGLU, T<=64)",
+        "kernel": "gemm1_decode_kernel (dispatch + GEMM1 + SwiGLU, T<=64; also routing for T<=8)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
         "algorithmic_bytes_per_launch": round(mean_bytes), "mean_launch_us": round(mean_us, 2),

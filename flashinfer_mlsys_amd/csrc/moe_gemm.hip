@@ -632,30 +632,6 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
 
-    // Waves 4-7 apply block kb's scales one iteration late (before their own
-    // MFMAs of kb+1). Each SIMD runs one wave of each half, so after the
-    // barrier one wave reads fragments and issues MFMAs while the other does
-    // VALU work, instead of both doing the same phase at once.
-    const bool late = wave >= Q1_WAVES / 2;
-    v4f pu[4][2], pg[4][2];
-    v4f sa_k[4];
-    float swu_k = 0.f, swg_k = 0.f;
-    auto scale_phase = [&]() {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        v4f fu, fg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { fu[r] = sa_k[mt][r] * swu_k; fg[r] = sa_k[mt][r] * swg_k; }
-#pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
-            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
-          }
-      }
-    };
-
     issue(0);
     issue(1);
 #pragma unroll 1
@@ -666,12 +642,12 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
       __builtin_amdgcn_s_barrier();  // every wave's loads for kb landed; kb-1 is fully read
       asm volatile("" ::: "memory");
       if (kb + 2 < NB_H) issue(kb + 2);
-      if (late && kb > 0) scale_phase();  // block kb-1
       const uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
-      // MFMA phase: all 16 products of this K block into their own registers
+      // MFMA phase: all 16 products of this K block into their own registers ...
       v8i a[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag_sw(st + (wm * 4 + mt) * FRAG_BYTES, flo, fhi);
+      v4f pu[4][2], pg[4][2];
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) {
         const v8i bu = lds_frag_sw(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
@@ -682,16 +658,24 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
           pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
         }
       }
-      // this block's scales (read now: the slot is refilled after the next barrier)
+      // ... then one fp32 FMA per accumulator with the block's activation x weight scale
+      const float swu = su[kb], swg = sg[kb];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        sa_k[mt] = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
-      swu_k = su[kb];
-      swg_k = sg[kb];
-      if (!late) scale_phase();
+      for (int mt = 0; mt < 4; ++mt) {
+        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
+        v4f fu, fg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
+#pragma unroll
+        for (int n2 = 0; n2 < 2; ++n2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
+            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
+          }
+      }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
     }
-    if (late) scale_phase();  // block 55
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
