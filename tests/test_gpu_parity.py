@@ -189,7 +189,7 @@ def test_forward_matches_reference(case):
     assert (out_np[~has] == 0).all()
 
 
-@pytest.mark.parametrize("case", ["decode_t1", "t16", "decode_t64"], indirect=True)
+@pytest.mark.parametrize("case", ["decode_t1", "decode_t8", "t16", "decode_t64"], indirect=True)
 def test_decode_and_prefill_shapes_agree(case):
     """T <= 64 runs the decode kernels by default; path 2 forces the prefill kernels."""
     old = fm.set_path(0)
@@ -262,7 +262,7 @@ def test_dps_writes_into_output(case):
     assert_close_bf16(out.float().cpu().numpy()[case.g["out_rows"]], ref, "dps")
 
 
-@pytest.mark.parametrize("case", ["decode_t1", "t16", "prefill_t1024"], indirect=True)
+@pytest.mark.parametrize("case", ["decode_t1", "decode_t8", "t16", "decode_t32", "prefill_t1024"], indirect=True)
 def test_graph_replay_matches_eager(case):
     """The forward captured in a HIP graph: every replay, with eager work and
     synchronisations between replays, gives the eager output bit for bit."""
@@ -281,6 +281,35 @@ def test_graph_replay_matches_eager(case):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
+
+
+def test_concurrent_streams_own_workspaces(weights, dev):
+    """Two callers on two streams (default priority), each with its own
+    workspace, interleaved: each output equals its single-stream eager output
+    bit for bit (the ABI is reentrant per workspace)."""
+    names = ["decode_t8", "prefill_t1024"]
+    ins, eager, outs, wss = [], [], [], []
+    for n in names:
+        w = wl.WORKLOADS[n]
+        acts = [a.to(dev) for a in wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)]
+        ins.append((acts, w))
+        e = fm.run(*acts, *weights[1], w.local_expert_offset, w.routed_scaling_factor)
+        torch.cuda.synchronize()
+        eager.append(e)
+        outs.append(torch.empty_like(e))
+        wss.append(torch.empty(fm.workspace_size(w.T), dtype=torch.uint8, device=dev))
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream(dev))
+    for _ in range(3):
+        for k in (0, 1):
+            acts, w = ins[k]
+            with torch.cuda.stream(streams[k]):
+                fm.kernel(*acts, *weights[1], w.local_expert_offset, w.routed_scaling_factor, outs[k],
+                          workspace=wss[k])
+    torch.cuda.synchronize()
+    for k in (0, 1):
+        assert torch.equal(outs[k].view(torch.int16), eager[k].view(torch.int16)), names[k]
 
 
 # --- producer-side activation quantiser ---------------------------------------
@@ -310,4 +339,25 @@ def test_quantize_activations_edge_cases(dev):
         rq, rs = cpu_ref.quantize_activations(x)
         np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), rq.view(torch.uint8).numpy())
         np.testing.assert_array_equal(s.cpu().numpy(), rs.numpy())
+
+
+def test_quantize_activations_graph_replay(dev):
+    """The quantiser captured in a HIP graph: each replay, with eager work in
+    between, reproduces the eager result."""
+    x = wl.hidden_bf16(37, 4).to(dev)
+    q = torch.empty((37, 7168), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((56, 37), dtype=torch.float32, device=dev)
+    fm.quantize_activations(x, out=(q, s))
+    torch.cuda.synchronize()
+    q0, s0 = q.clone(), s.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fm.quantize_activations(x, out=(q, s))
+    for i in range(3):
+        q.view(torch.uint8).fill_(0x55)
+        s.fill_(-1.0)
+        fm.quantize_activations(wl.hidden_bf16(16, 5).to(dev))  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8)) and torch.equal(s, s0), f"replay {i}"
 
