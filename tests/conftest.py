@@ -56,6 +56,67 @@ def assert_close_bf16(actual_f32, expected_f32, what=""):
 from oracle import np_ref  # noqa: E402  (test infrastructure)
 
 
+# --- GPU fixtures shared by the GPU test files (one weight upload per session) ---
+@pytest.fixture(scope="session")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def weights(dev):
+    """Expert weights (cpu, gpu), checked against the fingerprints the fixtures were made with."""
+    import json
+    from flashinfer_mlsys_amd import workloads as wl
+    print("generating expert weights", flush=True)
+    cpu = wl.make_weights()
+    with open(os.path.join(GOLDEN_DIR, "weights.json")) as f:
+        meta = json.load(f)
+    for t, k in zip(cpu, ["gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]):
+        assert wl.fingerprint(t) == meta[k], f"{k} does not regenerate identically on this host"
+    gpu = [t.to(dev) for t in cpu]
+    torch.cuda.synchronize()
+    return cpu, gpu
+
+
+# --- Trace-replay cases -----------------------------------------------------
+# Token counts and local-expert offsets of the official FlashInfer-Trace
+# workloads for this operator (input_analysis/input_check.ipynb cell 7: T from
+# 1 to 14107, offsets 0..224), with their routing-bias profile (every bias
+# 4.9375 or 4.96875, two adjacent bf16 values, cell 5). The uuids are the first
+# of "mi355x-trace-<T>-<offset>-<k>" whose routing has at least one local pair
+# and selection margins of at least 8 fp32 ulps (test_trace checks both).
+TRACE_CASES = [
+    ("mi355x-trace-7-192-0", 7, 192),
+    ("mi355x-trace-1-32-1", 1, 32),
+    ("mi355x-trace-80-96-0", 80, 96),
+    ("mi355x-trace-901-96-1", 901, 96),
+    ("mi355x-trace-16-224-0", 16, 224),
+    ("mi355x-trace-62-96-0", 62, 96),
+    ("mi355x-trace-14-0-0", 14, 0),
+    ("mi355x-trace-32-32-0", 32, 32),
+]
+
+
+def trace_case_tensors(uuid, T):
+    """Recorded inputs of a trace case: fp32 N(0,1) logits and the two-level bf16 bias."""
+    from flashinfer_mlsys_amd import trace, workloads as wl
+    seed = trace.TraceWorkload(uuid, T, {}).seed
+    logits = wl._normal((seed, 10), (T, 256), 1.0)
+    bits = np.random.Generator(np.random.PCG64([seed, 13])).integers(0, 2, 256)
+    bias = torch.from_numpy(4.9375 + 0.03125 * bits.astype(np.float32)).to(torch.bfloat16)
+    return logits, bias
+
+
+def write_trace_cases(root, cases=TRACE_CASES):
+    from flashinfer_mlsys_amd import trace
+    rows = []
+    for uuid, T, offset in cases:
+        lg, b = trace_case_tensors(uuid, T)
+        rows.append((uuid, T, offset, 2.5, {"routing_logits": lg, "routing_bias": b}))
+    return trace.write_trace_set(str(root), rows)
+
+
 def quant_edge_rows():
     """bf16 rows whose blocks have closed-form quantisations: a power-of-two scale
     (amax 448 * 2^-3) with every e4m3 value and every midpoint between two (ties);

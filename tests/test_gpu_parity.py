@@ -4,9 +4,6 @@ Bars: expert selection and the per-expert permutation bit-exact; the bf16 output
 within atol=1e-2, rtol=2e-2 (torch.allclose semantics) of the reference.
 Everything goes through libmoe_mi355x.so's C ABI via flashinfer_mlsys_amd.
 """
-import json
-import os
-
 import numpy as np
 import pytest
 import torch
@@ -15,7 +12,7 @@ import flashinfer_mlsys_amd as fm
 from flashinfer_mlsys_amd import workloads as wl
 from oracle import cpu_ref
 
-from conftest import GOLDEN_DIR, assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden, quant_edge_rows
+from conftest import assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden, quant_edge_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -25,25 +22,6 @@ SMALL = [n for n in ALL if wl.WORKLOADS[n].T <= 1024]
 
 def _say(msg):
     print(msg, flush=True)
-
-
-@pytest.fixture(scope="session")
-def dev():
-    assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
-    return torch.device("cuda:0")
-
-
-@pytest.fixture(scope="session")
-def weights(dev):
-    _say("generating expert weights")
-    cpu = wl.make_weights()
-    with open(os.path.join(GOLDEN_DIR, "weights.json")) as f:
-        meta = json.load(f)
-    for t, k in zip(cpu, ["gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"]):
-        assert wl.fingerprint(t) == meta[k], f"{k} does not regenerate identically on this host"
-    gpu = [t.to(dev) for t in cpu]
-    torch.cuda.synchronize()
-    return cpu, gpu
 
 
 class Case:
