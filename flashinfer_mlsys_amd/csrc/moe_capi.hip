@@ -22,8 +22,8 @@ hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, co
                                float*, int, hipStream_t);
 int gemm2_decode_blocks_per_cu();
 int gemm1_decode_blocks_per_cu();
-hipError_t launch_gemm1_tiled(const uint8_t*, const float*, int, const uint8_t*, const float*,
-                              const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
+hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*,
+                               const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_tiled(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
                               float*, int, hipStream_t);
 hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStream_t);
@@ -159,8 +159,8 @@ hipError_t run_stage(int stage, const Call& c) {
                                    c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr, c.perm_tok, c.perm_w,
                                    c.tok_pair, c.c_act, grid, c.stream);
       }
-      return launch_gemm1_tiled(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
-                                (cu_count() + 7) / 8 * 8, c.stream);
+      return launch_gemm1_loader(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
+                                 (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
       if (c.decode) {
         const int grid = std::min(max_active * (H / 32), cu_count() * gemm2_decode_blocks_per_cu());

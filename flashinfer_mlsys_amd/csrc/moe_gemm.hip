@@ -544,106 +544,203 @@ __device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
 
 // ---------------------------------------------------------------------------
 // GEMM1 + SwiGLU, prefill shape: 128 rows x 128 column pairs (X1 rows n..n+127
-// and X2 rows 2048+n..) per item, 8 waves as 2 (rows) x 4 (pairs); each wave
-// owns 64 rows x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles).
+// and X2 rows 2048+n..) per item. 8 compute waves as 2 (rows) x 4 (pairs); each
+// owns 64 rows x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles), and 4
+// loader waves move the operands.
 //
 // Operands go global -> LDS with the direct load (global_load_lds_dwordx4):
 // one wave instruction moves 64 lanes x 16 B and lane l's bytes land at
 // base + 16 l, with no staging registers. Each instruction loads 8 whole
 // 128 B row lines of a K block; the 16 B chunks are XOR-swizzled per row so
 // that the MFMA fragment reads (lds_frag_sw) are conflict-free. The activation
-// scales of the item's rows ride along.
-// Three LDS stages: the loads for K block kb+2 are issued while kb computes.
+// scales of the item's rows and the two weight block scales ride along.
+// Three LDS stages: the loads for K block kb+2 fly while kb computes.
 // ---------------------------------------------------------------------------
 constexpr int FRAG_BYTES = 2048;           // one 16 x 128 e4m3 fragment
 constexpr int Q1_BM = 128;
 constexpr int Q1_BNP = 128;
-constexpr int Q1_WAVES = 8;
 constexpr int Q1_NT = I / Q1_BNP;          // 16 column-pair tiles
 constexpr int Q1_AFR = Q1_BM / 16;         // 8 activation fragments per stage
 constexpr int Q1_BFR = 2 * Q1_BNP / 16;    // 16 weight fragments per stage (0-7 X1, 8-15 X2)
-constexpr int Q1_JOBS = 2 * (Q1_AFR + Q1_BFR) / Q1_WAVES;  // fragment halves per wave per stage: 6
 constexpr int Q1_SCALE_OFF = (Q1_AFR + Q1_BFR) * FRAG_BYTES;
-constexpr int Q1_STAGE = Q1_SCALE_OFF + Q1_BM * 4;
 constexpr int Q1_NSTAGE = 3;
-static_assert(2 * (Q1_AFR + Q1_BFR) % Q1_WAVES == 0, "even job split");
 
+// ---------------------------------------------------------------------------
+// Why loader waves: when every wave issued its own share of the loads right
+// after each K block's barrier, a wave waiting to issue loads into a busy
+// memory pipeline held back its MFMAs, and load time added to compute time.
+// With the global -> LDS traffic issued by 4 loader waves, the 8 compute waves
+// only read LDS and run MFMAs and the scale FMAs, and the 3-slot ring runs on
+// across items (the loaders fill the next item's first stages while the
+// compute waves finish the current one). One barrier per K
+// block: before it, each loader wave has waited for its own loads of that
+// block, each compute wave for its reads of the previous one.
+//
+// Loader wave p (0..3) moves, per K block, activation rows 32 p .. 32 p + 31
+// (4 half fragments), 8 of the 32 weight half fragments and the 32 activation
+// scales of its rows; the last one also the block's two weight scales (X1 and
+// X2 block rows), so the compute waves take every operand from LDS (a scalar
+// load in their loop would make them wait for all their LDS reads). Its rows' token indices come from scalar loads of
+// perm_tok: the 32 entries from row 32 p of the tile may run past the expert's
+// segment (up to 127 entries past the end of perm_tok, which the workspace
+// follows with the perm_w and C regions), and every row at or past the tile's
+// valid count takes the tile's first token instead.
+// ---------------------------------------------------------------------------
+constexpr int W1_CWAVES = 8;
+constexpr int W1_PWAVES = 4;
+constexpr int W1_THREADS = 64 * (W1_CWAVES + W1_PWAVES);
+constexpr int W1_AJOBS = 2 * Q1_AFR / W1_PWAVES;  // 4
+constexpr int W1_BJOBS = 2 * Q1_BFR / W1_PWAVES;  // 8
+constexpr int W1_WSCALE_OFF = Q1_SCALE_OFF + Q1_BM * 4;  // the two weight block scales of the K block
+constexpr int W1_STAGE = W1_WSCALE_OFF + 16;
+static_assert(W1_AJOBS == 4 && W1_BJOBS == 8 && Q1_BM == 32 * W1_PWAVES, "loader split");
 
-__global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
+// Spread scalar values over lanes: lane l of the result holds t[base + (l >> shift)]
+// for l < lanes (one v_writelane per lane; a select chain would be turned into an
+// indexed scratch table, whose loads count in vmcnt like the direct loads).
+// v_writelane ignores EXEC, so this must run in uniform control flow with every
+// lane active: the asm is volatile so that the compiler cannot sink it into a
+// divergent branch (where it would overwrite the inactive lanes too), and callers
+// compute every spread before any per-lane select of the results.
+template <int LANES, int SHIFT>
+__device__ __forceinline__ int spread_lanes(const int (&t)[32], int base) {
+  int v = 0;
+#pragma unroll
+  for (int l = 0; l < LANES; ++l)
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(t[base + (l >> SHIFT)]), "i"(l));
+  return v;
+}
+
+__global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
     const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q1_lds[];
-  __shared__ int sTok[Q1_BM];
   __shared__ TileMap map;
-  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
   build_tile_map<Q1_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
   const int total = tiled_items(total_m, Q1_NT);
-  int flo, fhi;
-  frag_sw_offsets(lane, flo, fhi);
-  static_assert(Q1_NT % TB_N == 0, "column blocks");
-
-  for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
+  const int first = xcd_remap(blockIdx.x, gridDim.x);
+  int n_items = 0;
+  for (int item = first; item < total; item += gridDim.x) {
     int mg, nt;
     tiled_item_coords(item, Q1_NT, mg, nt);
-    if (mg >= total_m) continue;  // uniform over the workgroup
+    n_items += mg < total_m;
+  }
+  const int G = n_items * NB_H;  // K blocks this workgroup runs, over all its items
+
+  if (wave >= W1_CWAVES) {
+    // ----------------------------- loader waves -----------------------------
+    const int p = wave - W1_CWAVES, rr = lane >> 3;
+    // the tile map in registers (lane e < 32 holds expert e's values), read before any
+    // direct load is in flight: later LDS reads would wait for every load in flight
+    const int my_pref = lane < E_LOCAL ? map.mt_prefix[lane] : 0;
+    const int my_next = lane < E_LOCAL ? map.mt_prefix[lane + 1] : 0x7fffffff;
+    const int my_cnt = lane < E_LOCAL ? map.cnt[lane] : 0;
+    const int my_seg = lane < E_LOCAL ? map.seg[lane] : 0;
+    const uint8_t* srcA[W1_AJOBS];
+    const uint8_t* srcB[W1_BJOBS];
+    const float* ssrc = hscale;
+    int sstride = T;
+    const bool scale_lane = lane < 32 || (p == W1_PWAVES - 1 && lane < 34);
+    int item = first - (int)gridDim.x, kb = NB_H, slot = 0;
+
+    auto next_item = [&]() {
+      int mg = 0, nt = 0;
+      for (item += gridDim.x; item < total; item += gridDim.x) {
+        tiled_item_coords(item, Q1_NT, mg, nt);
+        if (mg < total_m) break;
+      }
+      if (item >= total) return;
+      const int e = __popcll(__ballot(my_next <= mg));  // experts whose tiles all lie before mg
+      const int cnt = __builtin_amdgcn_readlane(my_cnt, e), seg = __builtin_amdgcn_readlane(my_seg, e);
+      const int m0 = (mg - __builtin_amdgcn_readlane(my_pref, e)) * Q1_BM;
+      const int valid = min(Q1_BM, cnt - m0);
+      const int32_t* tp = perm_tok + seg + m0;
+      int tk[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) tk[k] = tp[32 * p + k];
+      const int tok0 = tp[0];
+      // every spread first, with all lanes active (see spread_lanes), then the
+      // per-lane choice: rows at or past the valid count take the first token
+      int spread[W1_AJOBS];
+#pragma unroll
+      for (int i = 0; i < W1_AJOBS; ++i) spread[i] = spread_lanes<64, 3>(tk, 8 * i);
+      const int spread_s = spread_lanes<32, 0>(tk, 0);
+#pragma unroll
+      for (int i = 0; i < W1_AJOBS; ++i) {
+        const int r = 8 * i + rr, jj = i & 1;
+        const int tok = 32 * p + r < valid ? spread[i] : tok0;
+        srcA[i] = hidden + (size_t)tok * H + ((lane & 7) ^ rr ^ jj) * 16;
+      }
+#pragma unroll
+      for (int i = 0; i < W1_BJOBS; ++i) {
+        const int g = 4 * p + (i >> 1), jj = i & 1;
+        const int row = (g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16) + 8 * jj + rr;
+        srcB[i] = w13 + ((size_t)e * N1 + row) * H + ((lane & 7) ^ rr ^ jj) * 16;
+      }
+      const int q = lane & 31;
+      ssrc = hscale + (32 * p + q < valid ? spread_s : tok0);
+      sstride = T;
+      if (lane >= 32) {  // lanes 32, 33 of the last loader wave: X1 and X2 weight block scales
+        ssrc = s13 + ((size_t)e * NB_N1 + (lane == 32 ? nt : NB_I + nt)) * NB_H;
+        sstride = 1;
+      }
+      kb = 0;
+    };
+    auto issue = [&]() {
+      if (kb == NB_H) next_item();
+      uint8_t* st = q1_lds + slot * W1_STAGE;
+#pragma unroll
+      for (int i = 0; i < W1_AJOBS; ++i)
+        lds_direct16(srcA[i] + kb * BLK, st + (2 * p + (i >> 1)) * FRAG_BYTES + (i & 1) * 1024);
+#pragma unroll
+      for (int i = 0; i < W1_BJOBS; ++i)
+        lds_direct16(srcB[i] + kb * BLK, st + (Q1_AFR + 4 * p + (i >> 1)) * FRAG_BYTES + (i & 1) * 1024);
+      // lane l lands at + 4 l: the wave's 32 row scales, then (last wave) the weight scales
+      if (scale_lane) lds_direct4(ssrc + (size_t)kb * sstride, st + Q1_SCALE_OFF + 128 * p);
+      slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
+      ++kb;
+    };
+    if (G > 0) issue();
+    if (G > 1) issue();
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+      if (g + 1 < G) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");  // 13 loads per K block
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (g + 2 < G) issue();
+    }
+    return;
+  }
+
+  // ------------------------------- compute waves -------------------------------
+  const int fr = lane & 15, kg = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  int flo, fhi;
+  frag_sw_offsets(lane, flo, fhi);
+  int slot = 0;
+  for (int item = first; item < total; item += gridDim.x) {
+    int mg, nt;
+    tiled_item_coords(item, Q1_NT, mg, nt);
+    if (mg >= total_m) continue;
     const int e = find_expert(map, mg);
     const int m0 = (mg - map.mt_prefix[e]) * Q1_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
-    const int valid = min(Q1_BM, cnt - m0);
-    if (tid < Q1_BM) sTok[tid] = perm_tok[seg + m0 + min(tid, valid - 1)];
-    __syncthreads();
-
-    // This wave's load jobs: fragment f = job / 2, rows 8 (job % 2) .. +7 of it, for
-    // the jobs wave*6 .. wave*6+5 of the 48 per stage. Each job reads 8 whole
-    // 128 B row lines of the K block (lane l: row l / 8, chunk (l % 8) ^ swizzle).
-    const uint8_t* src[Q1_JOBS];
-    int dst[Q1_JOBS];
-#pragma unroll
-    for (int i = 0; i < Q1_JOBS; ++i) {
-      const int job = wave * Q1_JOBS + i, f = job >> 1, jj = job & 1;
-      const int rr = lane >> 3, koff = (((lane & 7) ^ rr ^ jj)) * 16;
-      if (f < Q1_AFR) {
-        src[i] = hidden + (size_t)sTok[f * 16 + 8 * jj + rr] * H + koff;
-      } else {
-        const int g = f - Q1_AFR;
-        const int row = (g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16) + 8 * jj + rr;
-        src[i] = w13 + ((size_t)e * N1 + row) * H + koff;
-      }
-      dst[i] = f * FRAG_BYTES + jj * 1024;
-    }
-    const float* ssrc = hscale + sTok[wave * 16 + (lane & 15)];
-    const float* su = s13 + ((size_t)e * NB_N1 + nt) * NB_H;          // X1 block row nt
-    const float* sg = s13 + ((size_t)e * NB_N1 + NB_I + nt) * NB_H;   // X2 block row 16 + nt
-
-    auto issue = [&](int kb) {
-      uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
-#pragma unroll
-      for (int i = 0; i < Q1_JOBS; ++i) lds_direct16(src[i] + kb * BLK, st + dst[i]);
-      if (lane < 16) lds_direct4(ssrc + (size_t)kb * T, st + Q1_SCALE_OFF + wave * 64);
-    };
-
     v4f accu[4][2], accg[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
-
-    issue(0);
-    issue(1);
 #pragma unroll 1
     for (int kb = 0; kb < NB_H; ++kb) {
-      // this wave's loads for K block kb are done (the next stage's 7 may still fly)
-      if (kb + 1 < NB_H) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();  // every wave's loads for kb landed; kb-1 is fully read
+      __builtin_amdgcn_s_barrier();  // K block kb is in its slot; the slot before it is free
       asm volatile("" ::: "memory");
-      if (kb + 2 < NB_H) issue(kb + 2);
-      const uint8_t* st = q1_lds + (kb % Q1_NSTAGE) * Q1_STAGE;
-      // MFMA phase: all 16 products of this K block into their own registers ...
+      const uint8_t* st = q1_lds + slot * W1_STAGE;
+      slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
       v8i a[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag_sw(st + (wm * 4 + mt) * FRAG_BYTES, flo, fhi);
@@ -658,8 +755,8 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
           pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
         }
       }
-      // ... then one fp32 FMA per accumulator with the block's activation x weight scale
-      const float swu = su[kb], swg = sg[kb];
+      const float swu = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF);
+      const float swg = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF + 4);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
@@ -674,7 +771,7 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
             accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
           }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -688,7 +785,6 @@ __global__ __launch_bounds__(64 * Q1_WAVES, 1) void gemm1_tiled_kernel(
             c_act[(size_t)(seg + row) * I + col] = f32_to_bf16_rne(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
           }
         }
-    __syncthreads();  // all waves are done with the LDS stages and sTok
   }
 }
 
@@ -959,17 +1055,17 @@ hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const f
   return hipGetLastError();
 }
 
-hipError_t launch_gemm1_tiled(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
-                              const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
-                              uint16_t* c_act, int grid, hipStream_t stream) {
+hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
+                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
+                               uint16_t* c_act, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_tiled_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * Q1_STAGE);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_loader_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * W1_STAGE);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(gemm1_tiled_kernel, dim3(grid), dim3(64 * Q1_WAVES), Q1_NSTAGE * Q1_STAGE, stream, hidden,
+  hipLaunchKernelGGL(gemm1_loader_kernel, dim3(grid), dim3(W1_THREADS), Q1_NSTAGE * W1_STAGE, stream, hidden,
                      hscale, T, w13, s13, hdr, perm_tok, c_act);
   return hipGetLastError();
 }

@@ -261,6 +261,26 @@ def test_graph_replay_matches_eager(case):
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
 
 
+@pytest.mark.parametrize("case", ["t16", "prefill_t1024", "skew_t4096"], indirect=True)
+def test_stale_workspace_is_never_read_as_data(case):
+    """The workspace arrives filled with 0xFF bytes (every stale token index reads
+    -1): the prefill kernels' partial row tiles read token entries past an expert's
+    segment and must replace them with a valid row, never load through them. The
+    output equals the one from a zeroed workspace, bit for bit."""
+    out = []
+    for fill in (0x00, 0xFF):
+        ws = torch.full((fm.workspace_size(case.w.T),), fill, dtype=torch.uint8, device=case.gpu[0].device)
+        o = torch.empty((case.w.T, 7168), dtype=torch.bfloat16, device=ws.device)
+        old = fm.set_path(2)  # the prefill kernels, whatever T
+        try:
+            fm.kernel(*case.gpu, case.offset, case.rsf, o, workspace=ws)
+            torch.cuda.synchronize()
+        finally:
+            fm.set_path(old)
+        out.append(o)
+    assert torch.equal(out[0].view(torch.int16), out[1].view(torch.int16))
+
+
 def test_concurrent_streams_own_workspaces(weights, dev):
     """Two callers on two streams (default priority), each with its own
     workspace, interleaved: each output equals its single-stream eager output
