@@ -24,8 +24,8 @@ int gemm2_decode_blocks_per_cu();
 int gemm1_decode_blocks_per_cu();
 hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*,
                                const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
-hipError_t launch_gemm2_tiled(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
-                              float*, int, hipStream_t);
+hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
+                               float*, int, hipStream_t);
 hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStream_t);
 }  // namespace moe
 
@@ -166,8 +166,8 @@ hipError_t run_stage(int stage, const Call& c) {
         const int grid = std::min(max_active * (H / 32), cu_count() * gemm2_decode_blocks_per_cu());
         return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, grid, c.stream);
       }
-      return launch_gemm2_tiled(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() + 7) / 8 * 8,
-                                c.stream);
+      return launch_gemm2_loader(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() + 7) / 8 * 8,
+                                 c.stream);
     case 3:
       return launch_combine(c.partial, c.tok_pair, c.T, c.out, c.stream);
     default:

@@ -791,8 +791,8 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
 // ---------------------------------------------------------------------------
 // GEMM2 (+ routing weight), prefill shape: 128 rows x 256 output columns per
 // item on the bf16 MFMA v_mfma_f32_32x32x16_bf16 (full bf16 rate; the 16x16x32
-// form runs at well under half of it), 8 waves as 2 (rows) x 4 (columns), each
-// 64 x 64 = 2 x 2 tiles of 32 x 32.
+// form runs at well under half of it), 8 compute waves as 2 (rows) x 4
+// (columns), each 64 x 64 = 2 x 2 tiles of 32 x 32, and 4 loader waves.
 //
 // One stage is one 128-wide K block (the W2 scale block): the activation tile
 // (128 rows x 256 B bf16) and the W2 tile (256 rows x 128 B e4m3), 64 KB, in a
@@ -808,15 +808,11 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
 // ---------------------------------------------------------------------------
 constexpr int Q2_BM = 128;
 constexpr int Q2_BN = 256;
-constexpr int Q2_WAVES = 8;
 constexpr int Q2_NT = H / Q2_BN;          // 28 column tiles
 constexpr int Q2_REG = 4096;              // 32 rows x 128 B
 constexpr int Q2_A_BYTES = Q2_BM * BLK * 2;  // 32 KB: 4 row blocks x 2 lines
 constexpr int Q2_B_BYTES = Q2_BN * BLK;      // 32 KB: 8 row blocks
 constexpr int Q2_STAGE = Q2_A_BYTES + Q2_B_BYTES;
-constexpr int Q2_NSTAGE = 2;
-constexpr int Q2_JOBS = (Q2_A_BYTES + Q2_B_BYTES) / 1024 / Q2_WAVES;  // 8 load instructions per wave per block
-static_assert(Q2_JOBS == 8, "load jobs");
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -832,87 +828,133 @@ __device__ __forceinline__ int sw32(int r, int c) {
   return j * 1024 + 16 * (8 * rr + (c ^ rr ^ (j & 1)));
 }
 
-__global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
+
+// ---------------------------------------------------------------------------
+// GEMM2 kernel: the item, stage layout and K order above, with the global ->
+// LDS traffic (64 load instructions per K block, 16 per loader wave: waves 0-1
+// the activation rows, 2-3 the W2 rows) issued by 4 loader waves while the 8
+// compute waves read LDS, widen W2 and run MFMAs (as in GEMM1, a wave that
+// issues loads would hold back its MFMAs while the memory pipeline is busy). The two 64 KB slots run on across items: after K block kb's barrier
+// the loaders fill the other slot with block kb + 1 (of this item or the next).
+// The last loader wave also carries the block's two W2 block scales (output
+// column blocks 2 nt and 2 nt + 1) into the stage.
+// ---------------------------------------------------------------------------
+constexpr int W2_CWAVES = 8;
+constexpr int W2_PWAVES = 4;
+constexpr int W2_THREADS = 64 * (W2_CWAVES + W2_PWAVES);
+constexpr int W2_LJOBS = (Q2_A_BYTES + Q2_B_BYTES) / 1024 / W2_PWAVES;  // 16 load instructions per loader wave
+constexpr int W2_WSCALE_OFF = Q2_STAGE;
+constexpr int W2_STAGE = Q2_STAGE + 16;
+static_assert(W2_LJOBS * W2_PWAVES == 64, "64 load instructions per K block");
+
+__global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
-  const int lr = lane & 31, lg = lane >> 5;
   build_tile_map<Q2_BM>(hdr, map);
   const int total_m = map.mt_prefix[E_LOCAL];
   const int total = tiled_items(total_m, Q2_NT);
-  static_assert(Q2_NT % TB_N == 0, "column blocks");
+  const int first = xcd_remap(blockIdx.x, gridDim.x);
+  int n_items = 0;
+  for (int item = first; item < total; item += gridDim.x) {
+    int mg, nt;
+    tiled_item_coords(item, Q2_NT, mg, nt);
+    n_items += mg < total_m;
+  }
+  const int G = n_items * NB_I;  // K blocks this workgroup runs
 
-  // fragment read offsets: W2 chunk 2 p + g for step pair p; activation chunk
-  // 4 (p % 2) + 2 g + (t % 2) of line p / 2 for step t = 2 p + t % 2
+  if (wave >= W2_CWAVES) {
+    // ----------------------------- loader waves -----------------------------
+    // Loads complete before every barrier (one block ahead, two slots), so these
+    // waves may read the tile map from LDS: no direct load is in flight then.
+    const int p = wave - W2_CWAVES, ld_row = lane >> 3;
+    const bool a_wave = p < 2;
+    const uint8_t* src[W2_LJOBS];
+    const float* ssrc = s2;
+    int item = first - (int)gridDim.x, kb = NB_I, slot = 0;
+    auto next_item = [&]() {
+      int mg = 0, nt = 0;
+      for (item += gridDim.x; item < total; item += gridDim.x) {
+        tiled_item_coords(item, Q2_NT, mg, nt);
+        if (mg < total_m) break;
+      }
+      const int e = find_expert(map, mg);
+      const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
+      const int cnt = map.cnt[e], seg = map.seg[e];
+#pragma unroll
+      for (int i = 0; i < W2_LJOBS; ++i) {
+        const int job = p * W2_LJOBS + i, rg = job & 3;
+        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
+        if (a_wave) {
+          const int ib = job >> 3, h = (job >> 2) & 1;
+          const int row = seg + min(m0 + ib * 32 + rg * 8 + ld_row, cnt - 1);
+          src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)row * I) + h * 128 + chunk * 16;
+        } else {
+          const int jb = (job - 32) >> 2;
+          src[i] = w2 + ((size_t)e * H + nt * Q2_BN + jb * 32 + rg * 8 + ld_row) * I + chunk * 16;
+        }
+      }
+      ssrc = s2 + ((size_t)e * NB_H + 2 * nt + (lane & 1)) * NB_I;
+      kb = 0;
+    };
+    auto issue = [&]() {
+      if (kb == NB_I) next_item();
+      uint8_t* st = q2_lds + slot * W2_STAGE;
+#pragma unroll
+      for (int i = 0; i < W2_LJOBS; ++i) {
+        const int job = p * W2_LJOBS + i, rg = job & 3;
+        const int dst = a_wave ? ((job >> 3) * 2 + ((job >> 2) & 1)) * Q2_REG + rg * 1024
+                               : Q2_A_BYTES + ((job - 32) >> 2) * Q2_REG + rg * 1024;
+        // activation rows advance 256 B per K block, W2 rows 128 B
+        lds_direct16(src[i] + (size_t)kb * (a_wave ? 2 * BLK : BLK), st + dst);
+      }
+      if (p == W2_PWAVES - 1 && lane < 2) lds_direct4(ssrc + kb, st + W2_WSCALE_OFF);
+      slot ^= 1;
+      ++kb;
+    };
+    if (G > 0) issue();
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block g
+      __builtin_amdgcn_s_barrier();                     // every block-g load landed; block g-1 is read
+      asm volatile("" ::: "memory");
+      if (g + 1 < G) issue();
+    }
+    return;
+  }
+
+  // ------------------------------- compute waves -------------------------------
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lr = lane & 31, lg = lane >> 5;
   int boff[4], aoff[2][2];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) boff[p] = sw32(lr, 2 * p + lg);
+  for (int pp = 0; pp < 4; ++pp) boff[pp] = sw32(lr, 2 * pp + lg);
 #pragma unroll
   for (int ph = 0; ph < 2; ++ph)
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) aoff[ph][tt] = sw32(lr, 4 * ph + 2 * lg + tt);
-  // this lane's place in a load instruction
-  const int ld_row = lane >> 3;
-
-  for (int item = xcd_remap(blockIdx.x, gridDim.x); item < total; item += gridDim.x) {
+  int slot = 0;
+  for (int item = first; item < total; item += gridDim.x) {
     int mg, nt;
     tiled_item_coords(item, Q2_NT, mg, nt);
-    if (mg >= total_m) continue;  // uniform over the workgroup
+    if (mg >= total_m) continue;
     const int e = find_expert(map, mg);
     const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
     const int cnt = map.cnt[e], seg = map.seg[e];
-
-    // Load jobs wave*8 .. wave*8+7: jobs 0-31 activations (row block jb / 8,
-    // line (jb / 4) % 2, rows 8 (jb % 4) ..), jobs 32-63 W2 (row block jb / 4,
-    // rows 8 (jb % 4) ..).
-    const uint8_t* src[Q2_JOBS];
-    int dst[Q2_JOBS];
-#pragma unroll
-    for (int i = 0; i < Q2_JOBS; ++i) {
-      const int job = wave * Q2_JOBS + i;
-      if (job < 32) {
-        const int ib = job >> 3, h = (job >> 2) & 1, rg = job & 3;
-        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
-        const int row = seg + min(m0 + ib * 32 + rg * 8 + ld_row, cnt - 1);
-        src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)row * I) + h * 128 + chunk * 16;
-        dst[i] = (ib * 2 + h) * Q2_REG + rg * 1024;
-      } else {
-        const int jb = (job - 32) >> 2, rg = job & 3;
-        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
-        src[i] = w2 + ((size_t)e * H + nt * Q2_BN + jb * 32 + rg * 8 + ld_row) * I + chunk * 16;
-        dst[i] = Q2_A_BYTES + jb * Q2_REG + rg * 1024;
-      }
-    }
-    const float* swp = s2 + ((size_t)e * NB_H + (nt * Q2_BN + wn * 64) / BLK) * NB_I;
-
-    auto issue = [&](int kb) {
-      uint8_t* st = q2_lds + (kb % Q2_NSTAGE) * Q2_STAGE;
-#pragma unroll
-      for (int i = 0; i < Q2_JOBS; ++i) {
-        // activation rows advance 256 B per K block, W2 rows 128 B
-        const int step = (wave * Q2_JOBS + i) < 32 ? 2 * BLK : BLK;
-        lds_direct16(src[i] + (size_t)kb * step, st + dst[i]);
-      }
-    };
-
     v16f acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
-
-    issue(0);
 #pragma unroll 1
     for (int kb = 0; kb < NB_I; ++kb) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for block kb
-      __builtin_amdgcn_s_barrier();  // everyone's block kb landed; block kb-1 fully read
+      __builtin_amdgcn_s_barrier();  // block kb is in its slot
       asm volatile("" ::: "memory");
-      if (kb + 1 < NB_I) issue(kb + 1);
-      const uint8_t* st = q2_lds + (kb % Q2_NSTAGE) * Q2_STAGE;
+      const uint8_t* st = q2_lds + slot * W2_STAGE;
+      slot ^= 1;
       const uint8_t* sa = st + (wm * 2) * 2 * Q2_REG;           // this wave's two activation row blocks
       const uint8_t* sb = st + Q2_A_BYTES + (wn * 2) * Q2_REG;  // its two W2 row blocks
       v16f pacc[2][2];
@@ -921,11 +963,11 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
 #pragma unroll
         for (int j = 0; j < 2; ++j) pacc[i][j] = v16f{};
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
+      for (int pp = 0; pp < 4; ++pp) {
         v8bf bf[2][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[p]);
+          const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[pp]);
           bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
           bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
         }
@@ -934,21 +976,21 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
           v8bf af[2];
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const v8bf*>(sa + (i * 2 + (p >> 1)) * Q2_REG + aoff[p & 1][tt]);
+            af[i] = *reinterpret_cast<const v8bf*>(sa + (i * 2 + (pp >> 1)) * Q2_REG + aoff[pp & 1][tt]);
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_bf16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
         }
       }
-      const float sc = swp[kb];
+      const float sc = *reinterpret_cast<const float*>(st + W2_WSCALE_OFF + 4 * (wn >> 1));
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] += pacc[i][j][r] * sc;
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // fragment reads done before the next barrier
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
     }
     // epilogue: weight by the pair's routing weight, one fp32 row per pair
 #pragma unroll
@@ -963,7 +1005,6 @@ __global__ __launch_bounds__(64 * Q2_WAVES, 1) void gemm2_tiled_kernel(
           for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
         }
       }
-    __syncthreads();  // the next item's first loads refill the slot of this item's last block
   }
 }
 
@@ -1070,17 +1111,17 @@ hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_tiled(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
-                              const float* perm_w, float* partial, int grid, hipStream_t stream) {
+hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
+                               const float* perm_w, float* partial, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_tiled_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q2_NSTAGE * Q2_STAGE);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_loader_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 2 * W2_STAGE);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL(gemm2_tiled_kernel, dim3(grid), dim3(64 * Q2_WAVES), Q2_NSTAGE * Q2_STAGE, stream, c_act, w2, s2,
-                     hdr, perm_w, partial);
+  hipLaunchKernelGGL(gemm2_loader_kernel, dim3(grid), dim3(W2_THREADS), 2 * W2_STAGE, stream, c_act, w2, s2, hdr,
+                     perm_w, partial);
   return hipGetLastError();
 }
 
