@@ -50,16 +50,25 @@ __device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, Sma
     if (lane == 0) d.cnt[le] = __popcll(m);
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, nact = 0;
-    for (int e = 0; e < E_LOCAL; ++e) {
-      d.seg[e] = acc;
-      if (d.cnt[e] > 0) d.active[nact++] = e;
-      acc += d.cnt[e];
+  if (wave == 0) {  // segment starts and the active list by one wave: lane e holds expert e
+    const int c = lane < E_LOCAL ? d.cnt[lane] : 0;
+    int incl = c;  // inclusive prefix sum over lanes
+#pragma unroll
+    for (int k = 1; k < E_LOCAL; k <<= 1) {
+      const int y = __shfl_up(incl, k);
+      if (lane >= k) incl += y;
     }
-    d.seg[E_LOCAL] = acc;
-    d.nact = nact;
-    for (int e = nact; e < E_LOCAL; ++e) d.active[e] = -1;
+    const unsigned long long act = __ballot(lane < E_LOCAL && c > 0);
+    const int nact = __popcll(act);
+    if (lane < E_LOCAL) {
+      d.seg[lane] = incl - c;
+      if (c > 0) d.active[__popcll(act & ((1ull << lane) - 1ull))] = lane;  // ascending ids
+      if (lane >= nact) d.active[lane] = -1;
+    }
+    if (lane == E_LOCAL - 1) {
+      d.seg[E_LOCAL] = incl;
+      d.nact = nact;
+    }
   }
   __syncthreads();
 }
