@@ -231,6 +231,31 @@ def test_zero_tokens(weights, dev):
     assert out.shape == (0, 7168)
 
 
+# (T, local_expert_offset, seed, routed_scaling_factor): token counts between the
+# benchmark's (3 and 9 around the in-GEMM1 routing limit of 8, 65 the first prefill
+# count, 100 and 257 partial row tiles, 513 one past a dispatch chunk of 512), other
+# offsets and a scaling factor of 1. Each seed is the first from 7000 + T whose
+# selection margins are at least 8 fp32 ulps and that routes a local pair.
+ODD_CASES = [(3, 0, 7003, 2.5), (9, 96, 7009, 2.5), (65, 224, 7065, 2.5), (100, 32, 7100, 1.0),
+             (257, 0, 7257, 2.5), (513, 160, 7513, 2.5)]
+
+
+@pytest.mark.parametrize("T,offset,seed,rsf", ODD_CASES)
+def test_odd_token_counts_match_oracle(weights, dev, T, offset, seed, rsf):
+    """Selection bit-exact and the whole output within the bar of the CPU oracle."""
+    _say(f"odd T={T} offset={offset} seed={seed} rsf={rsf}")
+    lg, b, hs, hss = wl.make_activations(T, seed, offset)
+    g, e = cpu_ref.selection_margins(lg, b)
+    assert min(g, e) >= 8, "the seed must keep the selection away from fp32 near-ties"
+    gpu = [t.to(dev) for t in (lg, b, hs, hss)] + list(weights[1])
+    ids, _, _ = fm.route(gpu[0], gpu[1], rsf)
+    ref_ids = cpu_ref.sorted_selection(cpu_ref.route(lg, b, rsf)[0])
+    assert torch.equal(ids.cpu().long(), ref_ids)
+    out = fm.run(*gpu, offset, rsf).float().cpu().numpy()
+    ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, rsf).float().numpy()
+    assert_close_bf16(out, ref, f"T={T} offset={offset}")
+
+
 @pytest.mark.parametrize("case", ["t16"], indirect=True)
 def test_dps_writes_into_output(case):
     out = torch.full((case.w.T, 7168), 7.0, dtype=torch.bfloat16, device=case.gpu[0].device)
