@@ -165,14 +165,59 @@ __device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __res
 }
 
 // This wave's K slice of rows m0..m0+15 of expert le (rows past cnt repeat the
-// last one) and their activation scales into LDS (only this wave reads them). Lane l's fragment bytes are
-// row l % 16, K 32 (l / 16) + [0, 32): half h holds bytes [16 h, 16 h + 16).
+// last one) and their activation scales, staged into LDS (only this wave reads
+// them) in two steps so that a caller can issue other loads in between: the
+// loads into registers, then the LDS writes, which wait only for these loads.
+// Lane l's fragment bytes are row l % 16, K 32 (l / 16) + [0, 32): half h holds
+// bytes [16 h, 16 h + 16). Plain loads and ds_writes, no direct-to-LDS loads:
+// the compiler cannot tell which LDS bytes a direct load writes, so every later
+// LDS read would wait for all loads in flight, the weight prefetches included.
+struct G1AStage {
+  v4i rows[D1_KPW][2];
+  float sc[2];
+};
+
+__device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const G1Shared& sh, const uint8_t* __restrict__ hidden,
+                                                const float* __restrict__ hscale, int T, int le, int m0, int wave) {
+  const SmallDispatch& d = sh.d;
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int cnt = d.cnt[le], seg = d.seg[le], kb0 = wave * D1_KPW;
+  // scales: entry i = 16 kk + r of the wave's block (lanes past 112 of the second load idle)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = lane + 64 * j;
+    a.sc[j] = 0.f;
+    if (i < D1_KPW * 16) {
+      const int kk = i >> 4, r = i & 15;
+      a.sc[j] = hscale[(size_t)(kb0 + kk) * T + d.tok[seg + min(m0 + r, cnt - 1)]];
+    }
+  }
+  const uint8_t* ap = hidden + (size_t)d.tok[seg + min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a.rows[kk][h] = *reinterpret_cast<const v4i*>(ap + kk * BLK + 16 * h);
+}
+
+__device__ __forceinline__ void g1_stage_a_store(const G1AStage& a, G1Shared& sh, int wave) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (lane + 64 * j < D1_KPW * 16) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = a.rows[kk][h];
+}
+
+// The same in one step, for a change of expert or a later 16-row pass inside the
+// run: the scales by 4 B direct loads (no registers held while the weight ring is
+// full), the rows through registers; the caller waits for the direct loads.
 __device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restrict__ hidden,
                                            const float* __restrict__ hscale, int T, int le, int m0, int wave) {
   const SmallDispatch& d = sh.d;
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
   const int cnt = d.cnt[le], seg = d.seg[le], kb0 = wave * D1_KPW;
-  // scales by 4 B direct loads: entry i = 16 kk + r of the wave's block, lanes past 112 masked
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = lane + 64 * j;
@@ -182,8 +227,6 @@ __device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restri
                   reinterpret_cast<uint8_t*>(&sh.sa[wave][0][0] + 64 * j));
     }
   }
-  // rows through registers (not direct loads: the compiler cannot tell which LDS
-  // bytes a direct load writes, so reads of sh.a would wait for every load in flight)
   const uint8_t* ap = hidden + (size_t)d.tok[seg + min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
 #pragma unroll
   for (int kk = 0; kk < D1_KPW; ++kk)
@@ -192,11 +235,6 @@ __device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restri
       *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = *reinterpret_cast<const v4i*>(ap + kk * BLK + 16 * h);
 }
 
-// One item with its weights in b (requested two items ago); requests item + 2
-// into b2 (always when PF, else if it exists). The steady-state loop uses PF so
-// that every path issues the same loads: the compiler's wait before the MFMAs
-// then lets the next two items' weights stay in flight (vmcnt(28)); with a
-// conditional request it has to assume none and waits for all of them.
 template <bool PF>
 __device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i (&b2)[D1_KPW], G1State& st,
                                         G1Shared& sh, const uint8_t* __restrict__ hidden,
@@ -209,6 +247,8 @@ __device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i
   const int le = __builtin_amdgcn_readfirstlane(d.active[item / D1_NT]), nt = item % D1_NT;
   const int cnt = __builtin_amdgcn_readfirstlane(d.cnt[le]), seg = __builtin_amdgcn_readfirstlane(d.seg[le]);
   const bool stage = !(st.a_resident && st.cur_le == le);  // uniform over the workgroup
+  // (the first item's rows are staged before the weight stream starts; a change
+  // of expert later in the run waits here for the weights already in flight)
   if (stage) g1_stage_a(sh, hidden, hscale, T, le, 0, wave);
   const int n2 = item + 2;
   const bool pf = PF || n2 < end;
@@ -294,20 +334,27 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const int total = sh.d.nact * D1_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int begin = blockIdx.x * per, end = min(total, begin + per);
-  const int kb0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * D1_KPW;
-  v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
-  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
-  if (ring) {
-    g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
-    g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
-  } else {
-    if (begin < end) g1_load_w(b0, w13, __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]), begin % D1_NT, kb0);
-    if (begin + 1 < end)
-      g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
-  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), kb0 = wave * D1_KPW;
+  // The token lists first (the first item's activation rows depend on them), then
+  // the first expert's rows are requested ahead of item 0's weights and written to
+  // LDS once those weight requests are out (the LDS writes wait only for the rows),
+  // then item 1's weights: the weight stream never drains before item 0.
   dispatch_small_lists(T, offset, sh.d);
   if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
   G1State st;
+  G1AStage a0;
+  const int le0 = begin < end ? __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]) : 0;
+  if (begin < end) g1_stage_a_load(a0, sh, hidden, hscale, T, le0, 0, wave);
+  v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
+  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
+  if (begin < end) {
+    g1_load_w(b0, w13, le0, begin % D1_NT, kb0);
+    g1_stage_a_store(a0, sh, wave);  // waits for the rows only (requested before item 0's weights)
+    st.cur_le = le0;
+    st.a_resident = sh.d.cnt[le0] <= 16;
+  }
+  if (ring || begin + 1 < end)
+    g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
   int item = begin;
   if (ring) {
     for (; item + 4 < end; item += 3) {  // items item+2..item+4 exist: unconditional requests
