@@ -420,6 +420,29 @@ __device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __rest
   }
 }
 
+// This wave's K slice (2 K blocks of bf16 C) of rows m0..m0+15 of expert le
+// (rows past cnt repeat the last one) into its LDS region, in two steps like the
+// GEMM1 staging: loads into registers, then LDS writes that wait only for them.
+struct G2AStage {
+  v4i q[D2_KPW][4];
+};
+__device__ __forceinline__ void g2_stage_a_load(G2AStage& a, const uint16_t* __restrict__ c_act, int seg, int cnt,
+                                                int m0, int kb0) {
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const uint16_t* ap = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
+#pragma unroll
+  for (int kk = 0; kk < D2_KPW; ++kk)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a.q[kk][q] = *reinterpret_cast<const v4i*>(ap + kk * BLK + 8 * q);
+}
+__device__ __forceinline__ void g2_stage_a_store(const G2AStage& a, G2Shared& sh, int wave) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int kk = 0; kk < D2_KPW; ++kk)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<v4i*>(&sh.a[wave][kk][q][lane * 16]) = a.q[kk][q];
+}
+
 template <bool PF>
 __device__ __forceinline__ void g2_item(int item, int end, v4i (&b)[D2_LD], v4i (&b2)[D2_LD], G2State& st, G2Shared& sh, const uint16_t* __restrict__ c_act,
                                         const uint8_t* __restrict__ w2, const float* __restrict__ s2,
@@ -436,12 +459,9 @@ __device__ __forceinline__ void g2_item(int item, int end, v4i (&b)[D2_LD], v4i 
 #pragma unroll
   for (int kk = 0; kk < D2_KPW; ++kk) sw[kk] = sp[kk];
   auto load_a = [&](int m0) {  // this wave's slice of rows m0..m0+15 into its own LDS region
-    const uint16_t* ap = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
-#pragma unroll
-    for (int kk = 0; kk < D2_KPW; ++kk)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<v4i*>(&sh.a[wave][kk][q][lane * 16]) = *reinterpret_cast<const v4i*>(ap + kk * BLK + 8 * q);
+    G2AStage a;
+    g2_stage_a_load(a, c_act, seg, cnt, m0, kb0);
+    g2_stage_a_store(a, sh, wave);
   };
   if (stage) load_a(0);
   if (PF || n2 < end) g2_load_w(b2, w2, __builtin_amdgcn_readfirstlane(sh.active[n2 / D2_NT]), n2 % D2_NT, kb0);
@@ -504,20 +524,37 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
   const int total = sh.nact * D2_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int begin = blockIdx.x * per, end = min(total, begin + per);
-  const int kb0 = __builtin_amdgcn_readfirstlane(tid >> 6) * D2_KPW;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kb0 = wave * D2_KPW;
   v4i b0[D2_LD], b1[D2_LD], b2[D2_LD];
   G2State st;
   const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
-  if (ring) {
-    g2_load_w(b0, w2, __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]), begin % D2_NT, kb0);
-    g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
-  } else {
-    if (begin < end) g2_load_w(b0, w2, __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]), begin % D2_NT, kb0);
-    if (begin + 1 < end)
-      g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
-  }
+  // The pair weights and the first expert's activation rows are requested ahead of
+  // item 0's weights and written to LDS once those weight requests are out (the
+  // writes wait only for them), then item 1's weights: no drain before item 0.
   const int P = sh.seg[E_LOCAL];
-  for (int p = tid; p < P; p += blockDim.x) sh.pw[p] = perm_w[p];
+  float pwv[SMALL_P / (64 * D2_WAVES)];
+#pragma unroll
+  for (int j = 0; j < SMALL_P / (64 * D2_WAVES); ++j) {
+    const int p = tid + j * 64 * D2_WAVES;
+    pwv[j] = p < P ? perm_w[p] : 0.f;
+  }
+  G2AStage a0;
+  const int le0 = begin < end ? __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]) : 0;
+  const int cnt0 = begin < end ? sh.cnt[le0] : 0;
+  if (begin < end) {
+    g2_stage_a_load(a0, c_act, sh.seg[le0], cnt0, 0, kb0);
+    g2_load_w(b0, w2, le0, begin % D2_NT, kb0);
+    g2_stage_a_store(a0, sh, wave);
+    st.cur_le = le0;
+    st.a_resident = cnt0 <= 16;
+  }
+  if (ring || begin + 1 < end)
+    g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
+#pragma unroll
+  for (int j = 0; j < SMALL_P / (64 * D2_WAVES); ++j) {
+    const int p = tid + j * 64 * D2_WAVES;
+    if (p < P) sh.pw[p] = pwv[j];
+  }
   __syncthreads();
   int item = begin;
   if (ring) {
