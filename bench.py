@@ -16,7 +16,8 @@ Printed JSON line (rank 0, one line):
                 between two HIP events on the operator's stream), against 8 TB/s
   cpu_baseline  the CPU oracle (PyTorch restatement of the reference, all 32 experts
                 dequantised per call as the reference does) timed on this host
-  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096)
+  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096) and the
+                producer-side kernels (FP8 activation quantiser, router GEMM) at T = 64 and 8192
 """
 from __future__ import annotations
 
@@ -365,6 +366,25 @@ def main():
                             "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
             log(f"quantize_activations T={T}: {us:.1f} us, {qa[f'T={T}']['GB_per_s']} GB/s")
         also["quantize_activations"] = qa
+        # producer side: the router GEMM (routing_logits = hidden_bf16 @ gate.T)
+        rl = {}
+        gate = wl.gate_weight_bf16().to(dev)
+        for T in (64, 8192):
+            x = wl.hidden_bf16(T, 78).to(dev)
+            lbuf = torch.empty((T, wl.E_GLOBAL), dtype=torch.float32, device=dev)
+            g = runner.graph(lambda: fm.router_logits(x, gate, out=lbuf), args.reps)
+            us = runner.graph_us(g, args.reps)
+            del g
+            nbytes = T * wl.H * 2 + wl.E_GLOBAL * wl.H * 2 + T * wl.E_GLOBAL * 4
+            flops = 2 * T * wl.E_GLOBAL * wl.H
+            rl[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
+                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                            "TFLOP_per_s": round(flops / (us * 1e-6) / 1e12, 1),
+                            "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
+            log(f"router_logits T={T}: {us:.1f} us, {rl[f'T={T}']['GB_per_s']} GB/s, "
+                f"{rl[f'T={T}']['TFLOP_per_s']} TFLOP/s")
+        also["router_logits"] = rl
 
     cpu = None
     if not args.no_cpu_baseline:

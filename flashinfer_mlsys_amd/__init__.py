@@ -25,8 +25,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_activations", "workspace_size",
-           "MoEInputError", "set_path"]
+__all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_activations", "router_logits",
+           "workspace_size", "MoEInputError", "set_path"]
 
 H = 7168
 I = 2048
@@ -202,6 +202,37 @@ def quantize_activations(hidden_bf16, out=None):
         code = _lib.load().moe_fp8_quantize_activations(x.data_ptr(), T, q.data_ptr(), scale.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_quantize_activations")
     return q, scale
+
+
+@torch.no_grad()
+def router_logits(hidden_bf16, gate_weight, out=None):
+    """Router GEMM: routing_logits fp32 [T, 256] = hidden_bf16 [T, 7168] x gate_weight^T,
+    gate_weight bf16 [256, 7168] (the linear layer that produces this operator's
+    routing_logits, reference moe/weight_origins_dataflow.md:21, :151-154). Products
+    are exact in fp32 and summed in fp32 in a fixed order. ``out`` may pass a
+    preallocated fp32 [T, 256] tensor."""
+    _on_gpu(hidden_bf16, "hidden_bf16")
+    _on_gpu(gate_weight, "gate_weight")
+    _req(hidden_bf16.dtype == torch.bfloat16 and hidden_bf16.dim() == 2 and hidden_bf16.shape[1] == H,
+         "hidden_bf16 must be bf16 [T, 7168]")
+    _req(gate_weight.dtype == torch.bfloat16 and tuple(gate_weight.shape) == (E_GLOBAL, H),
+         "gate_weight must be bf16 [256, 7168]")
+    _req(gate_weight.device == hidden_bf16.device, "gate_weight must be on the hidden states' device")
+    T = hidden_bf16.shape[0]
+    dev = hidden_bf16.device
+    if out is None:
+        out = torch.empty((T, E_GLOBAL), dtype=torch.float32, device=dev)
+    else:
+        _req(out.dtype == torch.float32 and tuple(out.shape) == (T, E_GLOBAL) and out.is_contiguous(),
+             "out must be a contiguous float32 [T, 256]")
+    if T == 0:
+        return out
+    x, g = _contig(hidden_bf16), _contig(gate_weight)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        code = lib.moe_fp8_router_logits(x.data_ptr(), g.data_ptr(), T, out.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_router_logits")
+    return out
 
 
 @torch.no_grad()

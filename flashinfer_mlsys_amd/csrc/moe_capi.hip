@@ -18,6 +18,7 @@ hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const
                                const uint8_t*, const float*, int32_t*, float*, DispatchHeader*, int32_t*, float*,
                                int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_quantize_1x128(const uint16_t*, int, uint8_t*, float*, hipStream_t);
+hipError_t launch_router_logits(const uint16_t*, const uint16_t*, int, float*, int, hipStream_t);
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
                                float*, int, hipStream_t);
 int gemm2_decode_blocks_per_cu();
@@ -274,6 +275,17 @@ int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t
   if (!aligned16(hidden_bf16) || !aligned16(hidden_states) || !aligned16(hidden_states_scale)) return MOE_ERR_ALIGN;
   hipError_t e = moe::launch_quantize_1x128(hidden_bf16, (int)T, hidden_states, hidden_states_scale,
                                             reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MOE_OK : hip_fail(e);
+}
+
+int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
+                          float* routing_logits, void* stream) {
+  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T == 0) return MOE_OK;
+  if (!hidden_bf16 || !gate_weight || !routing_logits) return MOE_ERR_NULL;
+  if (!aligned16(hidden_bf16) || !aligned16(gate_weight) || !aligned16(routing_logits)) return MOE_ERR_ALIGN;
+  hipError_t e = moe::launch_router_logits(hidden_bf16, gate_weight, (int)T, routing_logits, cu_count(),
+                                           reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 

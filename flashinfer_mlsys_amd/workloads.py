@@ -153,6 +153,15 @@ def hidden_bf16(T: int, seed: int):
     return _normal((seed, 12), (T, H), 1.0).to(torch.bfloat16)
 
 
+GATE_SEED = 20261202
+
+
+def gate_weight_bf16(seed: int = GATE_SEED):
+    """Router gate weights bf16 [256, 7168], N(0, 1/sqrt(7168)): with N(0, 1) hidden
+    states the logits come out N(0, 1), the benchmark's routing_logits distribution."""
+    return _normal((seed, 20), (E_GLOBAL, H), float(H) ** -0.5).to(torch.bfloat16)
+
+
 def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool = False):
     """(routing_logits fp32 [T,256], routing_bias bf16 [256], hidden e4m3 [T,H], hidden_scale [56,T])."""
     logits = _normal((seed, 10), (T, E_GLOBAL), 1.0)

@@ -133,6 +133,17 @@ int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_
 int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t* hidden_states,
                                  float* hidden_states_scale, void* stream);
 
+/*
+ * Router GEMM, the linear layer that produces this operator's routing_logits
+ * input (reference moe/weight_origins_dataflow.md:21, :151-154: "x @
+ * gate_weight.T (linear layer, no activation)"): routing_logits fp32 [T, 256] =
+ * hidden_bf16 [T, 7168] x gate_weight^T, gate_weight bf16 [256, 7168]; the
+ * products are exact in fp32 and summed in fp32 in a fixed order (the same
+ * logits on every call). All pointers 16-byte aligned. Stream-ordered.
+ */
+int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
+                          float* routing_logits, void* stream);
+
 /* Kernel shape used by moe_fp8_forward: 0 = by token count (default: the
  * decode shape for T <= 64, the prefill shape above), 1 = the same as 0
  * (the decode shape exists only for T <= 64), 2 = always the prefill shape.

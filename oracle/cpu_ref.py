@@ -63,6 +63,13 @@ def quantize_activations(x_bf16):
     return q.reshape(T, H), scale.t().contiguous()
 
 
+def router_logits(x_bf16, gate_weight):
+    """Router GEMM, ``reference moe/weight_origins_dataflow.md:21, :151-154``:
+    routing_logits [T, 256] fp32 = x [T, 7168] @ gate_weight.T ([256, 7168]), a linear
+    layer with no activation, on bf16 inputs computed in fp32."""
+    return x_bf16.to(torch.float32).matmul(gate_weight.to(torch.float32).t())
+
+
 def dequant_weight(w, s):
     """``ref_moe.py:80-92`` for one or more experts: W = fp8 * S[n/128, k/128] in fp32."""
     wf = w.to(torch.float32)

@@ -119,3 +119,20 @@ def e4m3_encode(x):
     pick_lo = (d_lo < d_hi) | ((d_lo == d_hi) & (pos_codes[lo] % 2 == 0))
     code = np.where(pick_lo, pos_codes[lo], pos_codes[hi]).astype(np.uint8)
     return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
+
+
+def router_logits_f64(x_bf16, gate_weight):
+    """x @ gate_weight.T in float64 from the bf16 bit patterns (independent of torch's
+    matmul): every bf16 x bf16 product is exact in float64 and the 7168-term sums
+    carry float64 rounding only. Returns (logits, sum over k of |x_k g_k|), the
+    second being the scale of any fp32 summation error."""
+    def f64(t):
+        bits = t.contiguous().cpu().view(_torch().int16).numpy()
+        return (bits.astype(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xf, gf = f64(x_bf16), f64(gate_weight)
+    return xf @ gf.T, np.abs(xf) @ np.abs(gf).T
+
+
+def _torch():
+    import torch
+    return torch

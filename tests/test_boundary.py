@@ -96,6 +96,18 @@ def test_quantize_argument_errors(lib):
     assert q(FAKE, 4, FAKE + 8, FAKE, None) == _lib.MOE_ERR_ALIGN
 
 
+def test_router_argument_errors(lib):
+    r = lib.moe_fp8_router_logits
+    assert r(FAKE, FAKE, 0, None, None) == _lib.MOE_OK  # nothing to do, nothing read
+    assert r(FAKE, FAKE, -1, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, (1 << 20) + 1, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(None, FAKE, 4, FAKE, None) == _lib.MOE_ERR_NULL
+    assert r(FAKE, None, 4, FAKE, None) == _lib.MOE_ERR_NULL
+    assert r(FAKE, FAKE, 4, None, None) == _lib.MOE_ERR_NULL
+    assert r(FAKE, FAKE + 8, 4, FAKE, None) == _lib.MOE_ERR_ALIGN
+    assert r(FAKE, FAKE, 4, FAKE + 4, None) == _lib.MOE_ERR_ALIGN
+
+
 def test_set_path(lib):
     assert lib.moe_fp8_set_path(7) == -1
     old = lib.moe_fp8_set_path(2)

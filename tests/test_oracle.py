@@ -218,3 +218,41 @@ def test_planted_mistakes_are_caught(monkeypatch, mutation):
     got = bf16_bits_to_f32(out.view(torch.int16).numpy().view(np.uint16)[g["out_rows"]])
     with pytest.raises(AssertionError):
         assert_close_bf16(got, bf16_bits_to_f32(g["out_bf16"]), mutation)
+
+
+def test_router_oracle_pins():
+    """cpu_ref.router_logits (torch fp32) against what fixes it independently: the
+    float64 restatement within the fp32 summation bound n u / (1 - n u) of sum |x g|
+    (n = 7168 terms); one-hot tokens give exactly one scaled gate column; a gate of
+    unit rows gives exactly the selected hidden columns."""
+    x, g = wl.hidden_bf16(7, 11), wl.gate_weight_bf16()
+    got = cpu_ref.router_logits(x, g).numpy().astype(np.float64)
+    ref, mag = np_ref.router_logits_f64(x, g)
+    n, u = 7168, 2.0 ** -24
+    assert (np.abs(got - ref) <= n * u / (1 - n * u) * mag).all()
+    assert abs(float(got.std()) - 1.0) < 0.2  # the benchmark's N(0, 1) logits scale
+    _router_closed_forms(cpu_ref.router_logits)
+
+
+def _router_closed_forms(fn):
+    g = wl.gate_weight_bf16()
+    ks = [0, 127, 128, 3000, 7167]
+    x1 = torch.zeros((len(ks), 7168), dtype=torch.bfloat16)
+    vals = torch.tensor([1.0, -2.5, 0.0078125, 3.0, -448.0], dtype=torch.bfloat16)
+    for i, k in enumerate(ks):
+        x1[i, k] = vals[i]
+    got = fn(x1, g)
+    exp = torch.stack([vals[i].float() * g[:, k].float() for i, k in enumerate(ks)])
+    assert torch.equal(got, exp), "one-hot tokens must give one gate column exactly"
+    idx = (torch.arange(256) * 28 + 5) % 7168
+    gu = torch.zeros((256, 7168), dtype=torch.bfloat16)
+    gu[torch.arange(256), idx] = 1.0
+    x = wl.hidden_bf16(3, 12)
+    assert torch.equal(fn(x, gu), x.float()[:, idx]), "unit gate rows must give the hidden columns exactly"
+
+
+def test_planted_router_mistake_is_caught():
+    """Experts taken in reverse order (a transposed or flipped gate index) fails the closed forms."""
+    with pytest.raises(AssertionError):
+        _router_closed_forms(lambda x, g: x.float().matmul(g.flip(0).float().t()))
+
