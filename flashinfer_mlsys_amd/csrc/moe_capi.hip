@@ -19,9 +19,8 @@ hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const
                                int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_quantize_1x128(const uint16_t*, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_router_logits(const uint16_t*, const uint16_t*, int, float*, int, hipStream_t);
-hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
-                               float*, int, hipStream_t);
-int gemm2_decode_blocks_per_cu();
+hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const int32_t*,
+                               const float*, int, uint16_t*, hipStream_t);
 int gemm1_decode_blocks_per_cu();
 hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*,
                                const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
@@ -138,8 +137,10 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
 
 // Stage 0: routing (+ dispatch in the prefill shape; nothing for a decode call
 // of at most 8 tokens, routed inside GEMM1); 1: GEMM1 + SwiGLU (+ the
-// in-workgroup dispatch in the decode shape); 2: GEMM2 x weight into one fp32
-// row per pair; 3: the ordered combine to bf16.
+// in-workgroup dispatch in the decode shape); 2: GEMM2 x weight (prefill: into
+// one fp32 row per pair; decode: with the ordered per-token sum, straight to the
+// bf16 output); 3: the ordered combine of the prefill rows to bf16 (nothing in
+// the decode shape).
 hipError_t run_stage(int stage, const Call& c) {
   using namespace moe;
   const int max_active = c.T * TOP_K < E_LOCAL ? c.T * TOP_K : E_LOCAL;
@@ -163,13 +164,11 @@ hipError_t run_stage(int stage, const Call& c) {
       return launch_gemm1_loader(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
                                  (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
-      if (c.decode) {
-        const int grid = std::min(max_active * (H / 32), cu_count() * gemm2_decode_blocks_per_cu());
-        return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, grid, c.stream);
-      }
+      if (c.decode) return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_tok, c.perm_w, c.T, c.out, c.stream);
       return launch_gemm2_loader(c.c_act, c.w2, c.s2, c.hdr, c.perm_w, c.partial, (cu_count() + 7) / 8 * 8,
                                  c.stream);
     case 3:
+      if (c.decode) return hipSuccess;  // summed inside GEMM2
       return launch_combine(c.partial, c.tok_pair, c.T, c.out, c.stream);
     default:
       return hipErrorInvalidValue;

@@ -356,47 +356,54 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2 x routing weight, decode shape (T <= 64): weighted fp32 partial rows,
-// summed per token by combine_kernel.
+// GEMM2 x routing weight + the ordered combine, decode shape (T <= 64).
 //
-// Same streaming structure as the decode GEMM1. Items are (active expert,
-// 32-column tile of the output): W2 rows n..n+31 as two MFMA column blocks of
-// the bf16 16x16x32 MFMA; each of the 8 waves owns 2 of the 16 K blocks. Lane
-// (fr, kg) reads 32 contiguous e4m3 bytes of a W2 row per K block and the same
-// 32 K values (bf16, 64 B) of its activation row, so step j of a block takes K
-// 32 kg + 8 j + [0, 8) in both operands. Weights stream through a 3-deep
-// register ring (items i+1 and i+2 in flight while item i computes); an
-// expert's activation slice (<= 16 rows) stays in the wave's own LDS region
-// across its items.
+// Workgroup c owns output columns 28 c .. 28 c + 27 (W2 rows; 256 workgroups
+// cover H = 7168 exactly, so every workgroup streams the same weight bytes) and
+// takes every active expert in ascending id: one item per expert, 28 W2 rows x
+// 2048 as two column blocks of the bf16 16x16x32 MFMA (the second block's last
+// 4 columns repeat row 27 and are dropped). Each of the 8 waves owns 2 of the 16
+// K blocks. Lane (fr, kg) reads 32 contiguous e4m3 bytes of a W2 row per K block
+// and the same 32 K values (bf16, 64 B) of its activation row, so step j of a
+// block takes K 32 kg + 8 j + [0, 8) in both operands. Weights stream through a
+// 3-deep register ring (items i+1 and i+2 in flight while item i computes); the
+// activation rows of item i+1 (the next expert's first 16 pairs) are loaded into
+// registers during item i, ahead of item i+2's weights.
+//
+// The cross-wave sum of an item's tile times the pair's routing weight is added
+// to its token's fp32 accumulator in LDS; items run in ascending expert id, so a
+// token's sum is 0 + v(e1) + v(e2) + ... in ascending expert order (the order of
+// ref_moe.py:164-166's accumulation over local experts). At the end the
+// workgroup writes its 28 columns of every token as bf16 (round to nearest
+// even), zeros for tokens without a local expert.
 // ---------------------------------------------------------------------------
 constexpr int D2_WAVES = 8;
-constexpr int D2_COLS = 32;
-constexpr int D2_NT = H / D2_COLS;       // 224 items per expert
+constexpr int D2_COLS = 28;
+constexpr int D2_NT = H / D2_COLS;       // 256 column chunks: the grid
 constexpr int D2_KPW = NB_I / D2_WAVES;  // 2 K blocks per wave
 constexpr int D2_LD = 2 * 2 * D2_KPW;    // 16 B weight loads per lane per item
-static_assert(NB_I % D2_WAVES == 0 && D2_COLS == 32, "tile shape");
+static_assert(H % D2_COLS == 0 && D2_NT == 256 && NB_I % D2_WAVES == 0, "tile shape");
+static_assert(D2_COLS % 4 == 0 && D2_COLS <= 32 && D2_COLS > 16, "two 16-column MFMA blocks, 4-column stores");
 
 struct G2Shared {
   int cnt[E_LOCAL];
   int seg[E_LOCAL + 1];
   int active[E_LOCAL];
   int nact;
-  float pw[SMALL_P];
+  float pw[SMALL_P];    // pair -> routing weight
+  int ptok[SMALL_P];    // pair -> token
   float red[2][D2_WAVES][2][4][64];
-  __attribute__((aligned(16))) uint8_t a[D2_WAVES][D2_KPW][4][1024];  // wave's activation slice, 16 B per lane
+  float acc[SMALL_T][32];  // token x column accumulators
 };
 
-struct G2State {
-  int cur_le = -1;
-  bool a_resident = false;
-  int phase = 0;
-};
-
-__device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __restrict__ w2, int le, int nt, int kb0) {
+// Weights of expert le for this workgroup's columns c0 .. c0 + 27, this wave's 2 K blocks.
+// Weights of expert le for this workgroup's columns c0 .. c0 + 27, this wave's 2 K blocks.
+__device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __restrict__ w2, int le, int c0, int kb0) {
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    const uint8_t* wp = w2 + ((size_t)le * H + nt * D2_COLS + cb * 16 + fr) * I + kb0 * BLK + kg * 32;
+    const int r = min(cb * 16 + fr, D2_COLS - 1);
+    const uint8_t* wp = w2 + ((size_t)le * H + c0 + r) * I + kb0 * BLK + kg * 32;
 #pragma unroll
     for (int kk = 0; kk < D2_KPW; ++kk) {
       b[(cb * D2_KPW + kk) * 2] = *reinterpret_cast<const v4i*>(wp + kk * BLK);
@@ -405,14 +412,13 @@ __device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __rest
   }
 }
 
-// This wave's K slice (2 K blocks of bf16 C) of rows m0..m0+15 of expert le
-// (rows past cnt repeat the last one) into its LDS region, in two steps like the
-// GEMM1 staging: loads into registers, then LDS writes that wait only for them.
-struct G2AStage {
+// This wave's K slice (2 K blocks of bf16 activations) of pair rows m0 .. m0 + 15
+// of an expert's segment (rows past cnt repeat the last one), in MFMA operand order.
+struct G2A {
   v4i q[D2_KPW][4];
 };
-__device__ __forceinline__ void g2_stage_a_load(G2AStage& a, const uint16_t* __restrict__ c_act, int seg, int cnt,
-                                                int m0, int kb0) {
+__device__ __forceinline__ void g2_load_a(G2A& a, const uint16_t* __restrict__ c_act, int seg, int cnt, int m0,
+                                          int kb0) {
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
   const uint16_t* ap = c_act + (size_t)(seg + min(m0 + fr, cnt - 1)) * I + kb0 * BLK + kg * 32;
 #pragma unroll
@@ -420,38 +426,37 @@ __device__ __forceinline__ void g2_stage_a_load(G2AStage& a, const uint16_t* __r
 #pragma unroll
     for (int q = 0; q < 4; ++q) a.q[kk][q] = *reinterpret_cast<const v4i*>(ap + kk * BLK + 8 * q);
 }
-__device__ __forceinline__ void g2_stage_a_store(const G2AStage& a, G2Shared& sh, int wave) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int kk = 0; kk < D2_KPW; ++kk)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<v4i*>(&sh.a[wave][kk][q][lane * 16]) = a.q[kk][q];
-}
 
+// Item k (expert active[k]): a holds its first 16 pair rows on entry and item
+// k + 1's on return; b holds its weights; b2 receives item k + 2's weights.
 template <bool PF>
-__device__ __forceinline__ void g2_item(int item, int end, v4i (&b)[D2_LD], v4i (&b2)[D2_LD], G2State& st, G2Shared& sh, const uint16_t* __restrict__ c_act,
-                                        const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-                                        float* __restrict__ partial) {
-  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
+__device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b)[D2_LD], v4i (&b2)[D2_LD],
+                                        int& phase, G2Shared& sh, const uint16_t* __restrict__ c_act,
+                                        const uint8_t* __restrict__ w2, const float* __restrict__ s2) {
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kb0 = wave * D2_KPW;
-  const int le = __builtin_amdgcn_readfirstlane(sh.active[item / D2_NT]), nt = item % D2_NT;
+  const int le = __builtin_amdgcn_readfirstlane(sh.active[k]);
   const int cnt = __builtin_amdgcn_readfirstlane(sh.cnt[le]), seg = __builtin_amdgcn_readfirstlane(sh.seg[le]);
-  const bool stage = !(st.a_resident && st.cur_le == le);
-  const int n2 = item + 2;
-  const float* sp = s2 + ((size_t)le * NB_H + (nt * D2_COLS) / BLK) * NB_I + kb0;  // wave-uniform: scalar loads
-  float sw[D2_KPW];
+  // block scales: the 28 columns touch the 128-row scale blocks of c0 and c0 + 27
+  const int blo = c0 / BLK, bhi = (c0 + D2_COLS - 1) / BLK;
+  const float* sp = s2 + (size_t)le * NB_H * NB_I + kb0;  // wave-uniform: scalar loads
+  float sw[2][D2_KPW];
 #pragma unroll
-  for (int kk = 0; kk < D2_KPW; ++kk) sw[kk] = sp[kk];
-  auto load_a = [&](int m0) {  // this wave's slice of rows m0..m0+15 into its own LDS region
-    G2AStage a;
-    g2_stage_a_load(a, c_act, seg, cnt, m0, kb0);
-    g2_stage_a_store(a, sh, wave);
-  };
-  if (stage) load_a(0);
-  if (PF || n2 < end) g2_load_w(b2, w2, __builtin_amdgcn_readfirstlane(sh.active[n2 / D2_NT]), n2 % D2_NT, kb0);
+  for (int kk = 0; kk < D2_KPW; ++kk) {
+    const float lo = sp[blo * NB_I + kk], hi = sp[bhi * NB_I + kk];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) sw[cb][kk] = (c0 + min(cb * 16 + fr, D2_COLS - 1)) / BLK == blo ? lo : hi;
+  }
+  G2A cur = a;
+  if (k + 1 < nact) {
+    const int ln = __builtin_amdgcn_readfirstlane(sh.active[k + 1]);
+    g2_load_a(a, c_act, __builtin_amdgcn_readfirstlane(sh.seg[ln]), __builtin_amdgcn_readfirstlane(sh.cnt[ln]), 0,
+              kb0);
+  }
+  if (PF || k + 2 < nact) g2_load_w(b2, w2, __builtin_amdgcn_readfirstlane(sh.active[k + 2]), c0, kb0);
   for (int m0 = 0; m0 < cnt; m0 += 16) {
-    if (m0 > 0) load_a(m0);
+    if (m0 > 0) g2_load_a(cur, c_act, seg, cnt, m0, kb0);
     v4f acc[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -463,39 +468,41 @@ __device__ __forceinline__ void g2_item(int item, int end, v4i (&b)[D2_LD], v4i 
         for (int j = 0; j < 4; ++j) {
           const v4i wq = b[(cb * D2_KPW + kk) * 2 + (j >> 1)];
           const v8bf wb = fp8x8_to_bf16x8((uint32_t)wq[2 * (j & 1)], (uint32_t)wq[2 * (j & 1) + 1]);
-          p = mfma_bf16_k32(*reinterpret_cast<const v8bf*>(&sh.a[wave][kk][j][lane * 16]), wb, p);
+          p = mfma_bf16_k32(__builtin_bit_cast(v8bf, cur.q[kk][j]), wb, p);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[cb][r] += p[r] * sw[kk];
+        for (int r = 0; r < 4; ++r) acc[cb][r] += p[r] * sw[cb][kk];
       }
     }
-    float(&red)[D2_WAVES][2][4][64] = sh.red[st.phase & 1];
+    float(&red)[D2_WAVES][2][4][64] = sh.red[phase & 1];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wave][cb][r][lane] = acc[cb][r];
     lds_barrier();
     {
+      // thread (row, col): pair row m0 + row, column col; MFMA lane (kg, fr) holds
+      // rows 4 kg + r, column fr of each column block
       const int row = tid >> 5, col = tid & 31, cb = col >> 4, r = row & 3, src = (row >> 2) * 16 + (col & 15);
-      float v = 0.f;
+      if (col < D2_COLS && m0 + row < cnt) {
+        float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < D2_WAVES; ++w) v += red[w][cb][r][src];
-      if (m0 + row < cnt) {
+        for (int w = 0; w < D2_WAVES; ++w) v += red[w][cb][r][src];
         const int pr = seg + m0 + row;
-        partial[(size_t)pr * H + nt * D2_COLS + col] = v * sh.pw[pr];
+        sh.acc[sh.ptok[pr]][col] += __fmul_rn(v, sh.pw[pr]);  // product rounded, then the sum
       }
     }
-    ++st.phase;
+    ++phase;
   }
-  st.cur_le = le;
-  st.a_resident = cnt <= 16;
 }
 
 __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+    const DispatchHeader* __restrict__ hdr, const int32_t* __restrict__ perm_tok, const float* __restrict__ perm_w,
+    int T, uint16_t* __restrict__ out) {
   __shared__ G2Shared sh;
   const int tid = threadIdx.x;
+  const int c0 = blockIdx.x * D2_COLS;
   if (tid < E_LOCAL) {
     sh.cnt[tid] = hdr->counts[tid];
     sh.seg[tid] = hdr->seg_start[tid];
@@ -505,56 +512,56 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     sh.seg[E_LOCAL] = hdr->seg_start[E_LOCAL];
     sh.nact = hdr->n_active;
   }
+  for (int i = tid; i < SMALL_T * 32; i += 64 * D2_WAVES) (&sh.acc[0][0])[i] = 0.f;
   __syncthreads();
-  const int total = sh.nact * D2_NT;
-  const int per = (total + gridDim.x - 1) / gridDim.x;
-  const int begin = blockIdx.x * per, end = min(total, begin + per);
+  const int nact = __builtin_amdgcn_readfirstlane(sh.nact);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kb0 = wave * D2_KPW;
   v4i b0[D2_LD], b1[D2_LD], b2[D2_LD];
-  G2State st;
-  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
-  // The pair weights and the first expert's activation rows are requested ahead of
-  // item 0's weights and written to LDS once those weight requests are out (the
-  // writes wait only for them), then item 1's weights: no drain before item 0.
+  G2A a;
+  int phase = 0;
+  const bool ring = nact >= 5;  // uniform: a steady state with unconditional requests
+  // The pair tokens and weights and the first expert's activation rows are
+  // requested ahead of item 0's weights, then item 1's weights; the pair tables go
+  // to LDS once those requests are out.
   const int P = sh.seg[E_LOCAL];
-  float pwv[SMALL_P / (64 * D2_WAVES)];
-#pragma unroll
-  for (int j = 0; j < SMALL_P / (64 * D2_WAVES); ++j) {
-    const int p = tid + j * 64 * D2_WAVES;
-    pwv[j] = p < P ? perm_w[p] : 0.f;
+  static_assert(SMALL_P <= 64 * D2_WAVES, "one pair per thread");
+  const float pwv = tid < P ? perm_w[tid] : 0.f;
+  const int ptv = tid < P ? perm_tok[tid] : 0;
+  if (nact > 0) {
+    const int le0 = __builtin_amdgcn_readfirstlane(sh.active[0]);
+    g2_load_a(a, c_act, __builtin_amdgcn_readfirstlane(sh.seg[le0]), __builtin_amdgcn_readfirstlane(sh.cnt[le0]), 0,
+              kb0);
+    g2_load_w(b0, w2, le0, c0, kb0);
   }
-  G2AStage a0;
-  const int le0 = begin < end ? __builtin_amdgcn_readfirstlane(sh.active[begin / D2_NT]) : 0;
-  const int cnt0 = begin < end ? sh.cnt[le0] : 0;
-  if (begin < end) {
-    g2_stage_a_load(a0, c_act, sh.seg[le0], cnt0, 0, kb0);
-    g2_load_w(b0, w2, le0, begin % D2_NT, kb0);
-    g2_stage_a_store(a0, sh, wave);
-    st.cur_le = le0;
-    st.a_resident = cnt0 <= 16;
-  }
-  if (ring || begin + 1 < end)
-    g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[(begin + 1) / D2_NT]), (begin + 1) % D2_NT, kb0);
-#pragma unroll
-  for (int j = 0; j < SMALL_P / (64 * D2_WAVES); ++j) {
-    const int p = tid + j * 64 * D2_WAVES;
-    if (p < P) sh.pw[p] = pwv[j];
+  if (nact > 1) g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[1]), c0, kb0);
+  if (tid < P) {
+    sh.pw[tid] = pwv;
+    sh.ptok[tid] = ptv;
   }
   __syncthreads();
-  int item = begin;
+  int k = 0;
   if (ring) {
-    for (; item + 4 < end; item += 3) {  // items item+2..item+4 exist
-      g2_item<true>(item, end, b0, b2, st, sh, c_act, w2, s2, partial);
-      g2_item<true>(item + 1, end, b1, b0, st, sh, c_act, w2, s2, partial);
-      g2_item<true>(item + 2, end, b2, b1, st, sh, c_act, w2, s2, partial);
+    for (; k + 4 < nact; k += 3) {  // items k+2..k+4 exist
+      g2_item<true>(k, nact, c0, a, b0, b2, phase, sh, c_act, w2, s2);
+      g2_item<true>(k + 1, nact, c0, a, b1, b0, phase, sh, c_act, w2, s2);
+      g2_item<true>(k + 2, nact, c0, a, b2, b1, phase, sh, c_act, w2, s2);
     }
   }
-  // the last (at most four) items; b0, b1 hold item, item + 1
-  if (item < end) g2_item<false>(item, end, b0, b2, st, sh, c_act, w2, s2, partial);
-  if (item + 1 < end) g2_item<false>(item + 1, end, b1, b0, st, sh, c_act, w2, s2, partial);
-  if (item + 2 < end) g2_item<false>(item + 2, end, b2, b1, st, sh, c_act, w2, s2, partial);
-  if (item + 3 < end) g2_item<false>(item + 3, end, b0, b2, st, sh, c_act, w2, s2, partial);
-
+  // the last (at most four) items; b0, b1 hold items k, k + 1
+  if (k < nact) g2_item<false>(k, nact, c0, a, b0, b2, phase, sh, c_act, w2, s2);
+  if (k + 1 < nact) g2_item<false>(k + 1, nact, c0, a, b1, b0, phase, sh, c_act, w2, s2);
+  if (k + 2 < nact) g2_item<false>(k + 2, nact, c0, a, b2, b1, phase, sh, c_act, w2, s2);
+  if (k + 3 < nact) g2_item<false>(k + 3, nact, c0, a, b0, b2, phase, sh, c_act, w2, s2);
+  __syncthreads();
+  // every token's 28 columns as bf16, 4 columns (8 B) per thread
+  for (int i = tid; i < T * (D2_COLS / 4); i += 64 * D2_WAVES) {
+    const int t = i / (D2_COLS / 4), c = (i % (D2_COLS / 4)) * 4;
+    const float* v = &sh.acc[t][c];
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
+    o.y = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
+    *reinterpret_cast<uint2*>(out + (size_t)t * H + c0 + c) = o;
+  }
 }
 
 
@@ -1135,20 +1142,12 @@ hipError_t launch_gemm1_decode(const float* logits, const uint16_t* bias, float 
   return hipGetLastError();
 }
 
-int gemm2_decode_blocks_per_cu() {
-  static int cached = 0;
-  if (cached > 0) return cached;
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm2_decode_kernel, 64 * D2_WAVES, 0) != hipSuccess || n < 1)
-    n = 1;
-  cached = n;
-  return n;
-}
-
 hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
-                               const float* perm_w, float* partial, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(grid), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr, perm_w,
-                     partial);
+                               const int32_t* perm_tok, const float* perm_w, int T, uint16_t* out,
+                               hipStream_t stream) {
+  if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(D2_NT), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr, perm_tok,
+                     perm_w, T, out);
   return hipGetLastError();
 }
 

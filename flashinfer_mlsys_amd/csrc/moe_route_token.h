@@ -15,6 +15,21 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 
 __device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
+// DPP lane moves within rows of 16 (gfx9 encodings): quad_perm [1,0,3,2] and
+// [2,3,0,1] are lane ^ 1 and lane ^ 2; half-row mirror maps lane i of each 8-lane
+// half to 7 - i; row mirror maps lane i of each row to 15 - i.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Number of the wave's keys (4 per lane) at or above t.
+__device__ __forceinline__ int count_ge(const uint32_t (&key)[4], uint32_t t) {
+  return popc_ballot(key[0] >= t) + popc_ballot(key[1] >= t) + popc_ballot(key[2] >= t) + popc_ballot(key[3] >= t);
+}
+
 // Routes token t with the calling wave (ref_moe.py:94-126). Lane l holds experts
 // 4l..4l+3, so the 8 lanes 8g..8g+7 hold routing group g.
 //  * scores: s = 1/(1+exp(-x)) with exp(-x) evaluated in fp64 and rounded once
@@ -23,9 +38,10 @@ __device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)
 //    over the group's 8 lanes); a group is kept when fewer than 4 groups beat it
 //    (larger score, or equal score and lower index).
 //  * the 8 experts are the 8 largest sb among the kept groups (others masked to
-//    the most negative finite float): the 8th largest key is found by a 32-step
-//    bitwise search on order-preserving keys with wave ballots + popcounts, then
-//    every key above it is taken plus the lowest-id keys equal to it.
+//    the most negative finite float): the 8th largest key (the largest t with at
+//    least 8 keys >= t) is found on order-preserving keys two bits per step, the
+//    three trial thresholds of a step counted independently with wave ballots +
+//    popcounts; then every key above it is taken plus the lowest-id keys equal to it.
 //  * weights = s / (sum of the 8 selected s + 1e-20) * rsf (unbiased s).
 // Writes, through generic pointers (global or LDS), the ascending selected ids
 // and their weights at ids[t*8 + pos], w[t*8 + pos]; tok_pair slots get -1.
@@ -48,14 +64,17 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
   float m1 = fmaxf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3]));
   float m2 = fmaxf(fminf(fmaxf(sb[0], sb[1]), fmaxf(sb[2], sb[3])),
                    fmaxf(fminf(sb[0], sb[1]), fminf(sb[2], sb[3])));
-#pragma unroll
-  for (int k = 1; k < 8; k <<= 1) {
-    const float o1 = __shfl_xor(m1, k);
-    const float o2 = __shfl_xor(m2, k);
+  // merge (largest, second largest) with lane ^ 1, lane ^ 2, then the mirrored
+  // half-row partner: every lane of the 8-lane group ends with the group's top 2
+  // (max and min only, so the result does not depend on the merge order).
+  auto merge = [&](float o1, float o2) {
     const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
     m1 = fmaxf(m1, o1);
     m2 = n2;
-  }
+  };
+  merge(dpp_f<DPP_XOR1>(m1), dpp_f<DPP_XOR1>(m2));
+  merge(dpp_f<DPP_XOR2>(m1), dpp_f<DPP_XOR2>(m2));
+  merge(dpp_f<DPP_HALF_MIRROR>(m1), dpp_f<DPP_HALF_MIRROR>(m2));
   const float gscore = m1 + m2;
   const int g = lane >> 3;
   int beaten = 0;
@@ -71,11 +90,10 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
   for (int i = 0; i < 4; ++i) key[i] = order_key(keep ? sb[i] : -3.402823466e+38f);
   uint32_t th = 0;
 #pragma unroll 4
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t trial = th | (1u << bit);
-    const int c = popc_ballot(key[0] >= trial) + popc_ballot(key[1] >= trial) + popc_ballot(key[2] >= trial) +
-                  popc_ballot(key[3] >= trial);
-    th = c >= TOP_K ? trial : th;
+  for (int bit = 30; bit >= 0; bit -= 2) {
+    const uint32_t t1 = th | (1u << bit), t2 = th | (2u << bit), t3 = th | (3u << bit);
+    const int c1 = count_ge(key, t1), c2 = count_ge(key, t2), c3 = count_ge(key, t3);
+    th = c3 >= TOP_K ? t3 : c2 >= TOP_K ? t2 : c1 >= TOP_K ? t1 : th;
   }
   const unsigned long long lt = (1ull << lane) - 1ull;
   bool sel[4], eq[4];
@@ -102,9 +120,17 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
     pos += __popcll(__ballot(sel[i]) & lt);
     ssum += sel[i] ? s[i] : 0.f;
   }
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) ssum += __shfl_xor(ssum, k);
-  const float denom = ssum + 1e-20f;
+  // sum over the wave: within each row of 16 (every lane of the row ends with the
+  // same value), then the four row sums in row order
+  ssum += dpp_f<DPP_XOR1>(ssum);
+  ssum += dpp_f<DPP_XOR2>(ssum);
+  ssum += dpp_f<DPP_HALF_MIRROR>(ssum);
+  ssum += dpp_f<DPP_MIRROR>(ssum);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 48));
+  const float denom = ((r0 + r1) + (r2 + r3)) + 1e-20f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (sel[i]) {
