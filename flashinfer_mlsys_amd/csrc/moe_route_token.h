@@ -25,9 +25,17 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Number of the wave's keys (4 per lane) at or above t.
-__device__ __forceinline__ int count_ge(const uint32_t (&key)[4], uint32_t t) {
-  return popc_ballot(key[0] >= t) + popc_ballot(key[1] >= t) + popc_ballot(key[2] >= t) + popc_ballot(key[3] >= t);
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// Compare-exchange of (key, slot) pairs into (larger key, or equal key and lower slot) first.
+__device__ __forceinline__ void cx(uint32_t& ka, int& ia, uint32_t& kb, int& ib) {
+  const bool sw = kb > ka || (kb == ka && ib < ia);
+  const uint32_t k = sw ? kb : ka, l = sw ? ka : kb;
+  const int i = sw ? ib : ia, j = sw ? ia : ib;
+  ka = k; kb = l; ia = i; ib = j;
 }
 
 // Routes token t with the calling wave (ref_moe.py:94-126). Lane l holds experts
@@ -38,10 +46,11 @@ __device__ __forceinline__ int count_ge(const uint32_t (&key)[4], uint32_t t) {
 //    over the group's 8 lanes); a group is kept when fewer than 4 groups beat it
 //    (larger score, or equal score and lower index).
 //  * the 8 experts are the 8 largest sb among the kept groups (others masked to
-//    the most negative finite float): the 8th largest key (the largest t with at
-//    least 8 keys >= t) is found on order-preserving keys two bits per step, the
-//    three trial thresholds of a step counted independently with wave ballots +
-//    popcounts; then every key above it is taken plus the lowest-id keys equal to it.
+//    the most negative finite float), ties to the lower id: each lane sorts its 4
+//    order-preserving keys (larger first, lower id first among equals); 8 rounds
+//    then take the wave maximum of the lanes' first keys, and the lowest lane
+//    holding it (which holds the lowest id with that key) selects that expert and
+//    drops it from its list.
 //  * weights = s / (sum of the 8 selected s + 1e-20) * rsf (unbiased s).
 // Writes, through generic pointers (global or LDS), the ascending selected ids
 // and their weights at ids[t*8 + pos], w[t*8 + pos]; tok_pair slots get -1.
@@ -85,34 +94,38 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
   }
   const bool keep = beaten < TOPK_GROUP;
 
-  uint32_t key[4];
+  // keys of finite floats are >= 0x00800000, so 0 marks an emptied list entry
+  uint32_t k0 = order_key(keep ? sb[0] : -3.402823466e+38f), k1 = order_key(keep ? sb[1] : -3.402823466e+38f);
+  uint32_t k2 = order_key(keep ? sb[2] : -3.402823466e+38f), k3 = order_key(keep ? sb[3] : -3.402823466e+38f);
+  int i0 = 0, i1 = 1, i2 = 2, i3 = 3;
+  cx(k0, i0, k1, i1);
+  cx(k2, i2, k3, i3);
+  cx(k0, i0, k2, i2);
+  cx(k1, i1, k3, i3);
+  cx(k1, i1, k2, i2);
+  uint32_t selmask = 0;  // bit i: this lane's expert 4 lane + i is selected
 #pragma unroll
-  for (int i = 0; i < 4; ++i) key[i] = order_key(keep ? sb[i] : -3.402823466e+38f);
-  uint32_t th = 0;
-#pragma unroll 4
-  for (int bit = 30; bit >= 0; bit -= 2) {
-    const uint32_t t1 = th | (1u << bit), t2 = th | (2u << bit), t3 = th | (3u << bit);
-    const int c1 = count_ge(key, t1), c2 = count_ge(key, t2), c3 = count_ge(key, t3);
-    th = c3 >= TOP_K ? t3 : c2 >= TOP_K ? t2 : c1 >= TOP_K ? t1 : th;
-  }
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  bool sel[4], eq[4];
-  int n_gt = 0, eq_below = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    sel[i] = key[i] > th;
-    eq[i] = key[i] == th;
-    n_gt += popc_ballot(sel[i]);
-    eq_below += __popcll(__ballot(eq[i]) & lt);
-  }
-  const int need = TOP_K - n_gt;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (eq[i]) {
-      sel[i] = eq_below < need;
-      ++eq_below;
+  for (int r = 0; r < TOP_K; ++r) {
+    uint32_t m = k0;  // wave maximum of the lists' first keys: within rows of 16, then the 4 rows
+    m = max(m, dpp_u<DPP_XOR1>(m));
+    m = max(m, dpp_u<DPP_XOR2>(m));
+    m = max(m, dpp_u<DPP_HALF_MIRROR>(m));
+    m = max(m, dpp_u<DPP_MIRROR>(m));
+    const uint32_t mx = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+                            max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+    const int win = __builtin_ctzll(__ballot(k0 == mx));  // lowest lane: lowest id with that key
+    if (lane == win) {
+      selmask |= 1u << i0;
+      k0 = k1; i0 = i1;
+      k1 = k2; i1 = i2;
+      k2 = k3; i2 = i3;
+      k3 = 0u;
     }
   }
+  bool sel[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sel[i] = (selmask >> i) & 1u;
+  const unsigned long long lt = (1ull << lane) - 1ull;
   int pos = 0;
   float ssum = 0.f;
 #pragma unroll

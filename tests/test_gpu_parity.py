@@ -10,7 +10,7 @@ import torch
 
 import flashinfer_mlsys_amd as fm
 from flashinfer_mlsys_amd import workloads as wl
-from oracle import cpu_ref
+from oracle import cpu_ref, np_ref
 
 from conftest import assert_close_bf16, bf16_bits_to_f32, golden_lists, load_golden, quant_edge_rows
 
@@ -52,6 +52,34 @@ def case(request, weights, dev):
         _cases.clear()
         _cases[name] = Case(name, weights, dev)
     return _cases[name]
+
+
+# logits whose float32 sigmoid is the same whether exp(-x) is rounded from float64
+# (the kernel) or evaluated in float32 (numpy), so both sides see identical keys
+TIE_LOGITS = np.array([-0.5, 0.0, 0.25, 0.5, 0.75, 1.0, 2.0, 3.0], dtype=np.float32)
+TIE_BIAS = np.array([0.0, 0.25, 0.5], dtype=np.float32)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 300])
+def test_route_ties_break_to_lower_id(dev, T):
+    """Logits and bias from a few values, so equal keys meet at the group cut and
+    at the 8th expert everywhere: the selection must be the independent
+    restatement's (equal group scores keep the lower group, equal keys the lower
+    expert id), bit for bit."""
+    one = np.float32(1.0)
+    s32 = one / (one + np.exp(-TIE_LOGITS))
+    s64 = one / (one + np.exp(-TIE_LOGITS.astype(np.float64)).astype(np.float32))
+    assert (s32 == s64).all()
+    rng = np.random.default_rng(4242 + T)
+    lg = TIE_LOGITS[rng.integers(0, len(TIE_LOGITS), size=(T, 256))]
+    b = TIE_BIAS[rng.integers(0, len(TIE_BIAS), size=256)]
+    ids, w, _ = fm.route(torch.from_numpy(lg).to(dev), torch.from_numpy(b).to(torch.bfloat16).to(dev), 2.5)
+    ref_ids, ref_w = np_ref.brute_force_route(lg, b, 2.5)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids.astype(np.int32))
+    np.testing.assert_allclose(w.cpu().numpy(), ref_w, rtol=4e-7 * 8, atol=0)
+    # every key equal: groups 0-3 kept, experts 0-7 selected
+    eq, _, _ = fm.route(torch.ones((T, 256), device=dev), torch.zeros(256, dtype=torch.bfloat16, device=dev), 2.5)
+    assert (eq.cpu().numpy() == np.arange(8, dtype=np.int32)).all()
 
 
 @pytest.mark.parametrize("case", ALL, indirect=True)
