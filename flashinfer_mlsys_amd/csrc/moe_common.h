@@ -71,6 +71,15 @@ __device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& o0, uint32
   o1 = pack_bf16_hi(b[0], b[1]);
 }
 
+// Barrier for LDS traffic only. __syncthreads() also orders global memory, and
+// since global stores count in vmcnt like loads, it waits for every load in
+// flight (prefetched weights, say) whenever a store precedes it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // fp32 -> bf16 bits, round to nearest even (quiet NaN kept NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);

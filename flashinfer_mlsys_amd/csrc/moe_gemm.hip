@@ -81,14 +81,6 @@ __device__ __forceinline__ v8i lds_frag_sw(const uint8_t* f, int lo, int hi) {
   return r;
 }
 
-// Barrier for LDS traffic only. __syncthreads() also orders global memory, and
-// since global stores count in vmcnt like loads, it waits for every load in
-// flight (here: prefetched weights) whenever a store precedes it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 __device__ __forceinline__ v8i lds_frag(const uint8_t* f) {
   const int lane = threadIdx.x & 63;
   const v4i lo = *reinterpret_cast<const v4i*>(f + lane * 16);
@@ -132,7 +124,8 @@ struct G1Shared {
   SmallDispatch d;
   float red[2][D1_WAVES][4][64];
   __attribute__((aligned(16))) uint8_t a[D1_WAVES][D1_KPW][2][1024];  // wave's K slice, 16 rows, fragment halves
-  __attribute__((aligned(16))) float sa[D1_WAVES][D1_KPW][16];        // their activation scales
+  __attribute__((aligned(16))) float sa[D1_WAVES][D1_KPW + 1][16];    // their activation scales (+16 padding)
+  int tok0[D1_WAVES][16];  // per wave: the first expert's first 16 tokens (prologue)
 };
 
 struct G1State {
@@ -162,11 +155,12 @@ struct G1AStage {
   float sc[2];
 };
 
-__device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const G1Shared& sh, const uint8_t* __restrict__ hidden,
-                                                const float* __restrict__ hscale, int T, int le, int m0, int wave) {
-  const SmallDispatch& d = sh.d;
+// (tok: the expert's ascending token list, at least min(cnt, m0 + 16) entries)
+__device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const int* tok, int cnt,
+                                                const uint8_t* __restrict__ hidden,
+                                                const float* __restrict__ hscale, int T, int m0, int wave) {
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
-  const int cnt = d.cnt[le], seg = d.seg[le], kb0 = wave * D1_KPW;
+  const int kb0 = wave * D1_KPW;
   // scales: entry i = 16 kk + r of the wave's block (lanes past 112 of the second load idle)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -174,10 +168,10 @@ __device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const G1Shared& sh,
     a.sc[j] = 0.f;
     if (i < D1_KPW * 16) {
       const int kk = i >> 4, r = i & 15;
-      a.sc[j] = hscale[(size_t)(kb0 + kk) * T + d.tok[seg + min(m0 + r, cnt - 1)]];
+      a.sc[j] = hscale[(size_t)(kb0 + kk) * T + tok[min(m0 + r, cnt - 1)]];
     }
   }
-  const uint8_t* ap = hidden + (size_t)d.tok[seg + min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
+  const uint8_t* ap = hidden + (size_t)tok[min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
 #pragma unroll
   for (int kk = 0; kk < D1_KPW; ++kk)
 #pragma unroll
@@ -187,12 +181,57 @@ __device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const G1Shared& sh,
 __device__ __forceinline__ void g1_stage_a_store(const G1AStage& a, G1Shared& sh, int wave) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-    if (lane + 64 * j < D1_KPW * 16) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];
+  for (int j = 0; j < 2; ++j) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];  // lanes past 112: padding
 #pragma unroll
   for (int kk = 0; kk < D1_KPW; ++kk)
 #pragma unroll
     for (int h = 0; h < 2; ++h) *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = a.rows[kk][h];
+}
+
+// Buffer loads for the prologue: a wave-uniform resource (base, byte range) in
+// SGPRs, a 32-bit offset per lane. With a range of 0 the loads return zeros
+// without a memory access, so the prologue's requests are unconditional: with a
+// branch around them the compiler could not count the requests in flight past
+// the branch and would wait for all of them before the first LDS work after it.
+// Word 3 is the gfx9 raw-buffer format (32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// g1_load_w and g1_stage_a_load for the prologue (zeros, no traffic, when !valid).
+__device__ __forceinline__ void g1_load_w_pro(v8i (&b)[D1_KPW], const uint8_t* __restrict__ w13, int le, int nt,
+                                              int kb0, bool valid) {
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int wrow = fr < 8 ? nt * 8 + fr : I + nt * 8 + (fr - 8);
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(w13 + (size_t)le * N1 * H + kb0 * BLK, valid ? (uint32_t)N1 * H : 0u);
+  const uint32_t off = (uint32_t)(wrow * H + kg * 32);
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk) {
+    const v4i lo = buf_load16(r, off + kk * BLK), hi = buf_load16(r, off + kk * BLK + 16);
+    b[kk] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+}
+__device__ __forceinline__ void g1_stage_a_load_pro(G1AStage& a, const int* tok, int cnt,
+                                                    const uint8_t* __restrict__ hidden,
+                                                    const float* __restrict__ hscale, int T, int wave, bool valid) {
+  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int kb0 = wave * D1_KPW;
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(hscale, valid ? (uint32_t)(NB_H * T * 4) : 0u);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = lane + 64 * j, kk = (i >> 4) % D1_KPW, r = i & 15;
+    const uint32_t off = (uint32_t)(((kb0 + kk) * T + tok[max(min(r, cnt - 1), 0)]) * 4);
+    a.sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+  }
+  const __amdgpu_buffer_rsrc_t rr = buf_rsrc(hidden + kb0 * BLK, valid ? (uint32_t)(T * H) : 0u);
+  const uint32_t off = (uint32_t)(tok[max(min(fr, cnt - 1), 0)] * H + kg * 32);
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a.rows[kk][h] = buf_load16(rr, off + kk * BLK + 16 * h);
 }
 
 // The same in one step, for a change of expert or a later 16-row pass inside the
@@ -304,42 +343,52 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
     float* __restrict__ perm_w, int32_t* __restrict__ tok_pair, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t g1d_lds[];
   G1Shared& sh = *reinterpret_cast<G1Shared*>(g1d_lds);
+  const int lane = threadIdx.x & 63;
   if (route_here) {
     const int w = threadIdx.x >> 6;
     if (w < T) route_token(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr);
-    __syncthreads();
+    lds_barrier();
     if (blockIdx.x == 0 && (int)threadIdx.x < T * TOP_K) {
       topk_ids[threadIdx.x] = sh.d.ids[threadIdx.x];
       topk_w[threadIdx.x] = sh.d.wts[threadIdx.x];
     }
-    dispatch_small_counts_lds(T, offset, sh.d);
   } else {
-    dispatch_small_counts(topk_ids, topk_w, T, offset, sh.d);
+    dispatch_small_ids(topk_ids, topk_w, T, sh.d);
   }
-  const int total = sh.d.nact * D1_NT;
+  dispatch_small_masks(T, offset, sh.d);
+  // The workgroup's items follow from the active set alone, and the first item's
+  // activation rows from the token masks: the first expert's rows, then item 0's
+  // and item 1's weights are requested before the rest of the dispatch (counts,
+  // segments, lists, pair indices) is built in LDS, while they fly. The rows are
+  // written to LDS once item 0's weight requests are out (the writes wait only for
+  // the rows), so the weight stream never drains before item 0.
+  const uint32_t act = small_active_set(T, sh.d);
+  const int total = __popc(act) * D1_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
   const int begin = blockIdx.x * per, end = min(total, begin + per);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), kb0 = wave * D1_KPW;
-  // The token lists first (the first item's activation rows depend on them), then
-  // the first expert's rows are requested ahead of item 0's weights and written to
-  // LDS once those weight requests are out (the LDS writes wait only for the rows),
-  // then item 1's weights: the weight stream never drains before item 0.
-  dispatch_small_lists(T, offset, sh.d);
-  if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
   G1State st;
   G1AStage a0;
-  const int le0 = begin < end ? __builtin_amdgcn_readfirstlane(sh.d.active[begin / D1_NT]) : 0;
-  if (begin < end) g1_stage_a_load(a0, sh, hidden, hscale, T, le0, 0, wave);
+  const bool has0 = begin < end, ring = end - begin >= 5, has1 = ring || begin + 1 < end;  // uniform
+  const int le0 = has0 ? nth_set_bit(act, begin / D1_NT) : 0;
+  const int le1 = has1 ? nth_set_bit(act, (begin + 1) / D1_NT) : 0;
+  const bool in0 = lane < T && ((sh.d.mask[lane] >> le0) & 1u);  // token `lane` routes to le0
+  const unsigned long long m0 = __ballot(in0);
+  const int cnt0 = __popcll(m0), rank = __popcll(m0 & ((1ull << lane) - 1ull));
+  if (in0 && rank < 16) sh.tok0[wave][rank] = lane;  // this wave's copy, read only by this wave
+  if (lane == 0 && cnt0 == 0) sh.tok0[wave][0] = 0;  // (no item: any valid index)
+  g1_stage_a_load_pro(a0, &sh.tok0[wave][0], cnt0, hidden, hscale, T, wave, has0);
+  __builtin_amdgcn_sched_barrier(0);  // the rows are requested ahead of the weights
   v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
-  const bool ring = end - begin >= 5;  // uniform: a steady state with unconditional requests
-  if (begin < end) {
-    g1_load_w(b0, w13, le0, begin % D1_NT, kb0);
-    g1_stage_a_store(a0, sh, wave);  // waits for the rows only (requested before item 0's weights)
-    st.cur_le = le0;
-    st.a_resident = sh.d.cnt[le0] <= 16;
-  }
-  if (ring || begin + 1 < end)
-    g1_load_w(b1, w13, __builtin_amdgcn_readfirstlane(sh.d.active[(begin + 1) / D1_NT]), (begin + 1) % D1_NT, kb0);
+  g1_load_w_pro(b0, w13, le0, begin % D1_NT, kb0, has0);
+  g1_stage_a_store(a0, sh, wave);  // waits for the rows only (requested before item 0's weights)
+  st.cur_le = le0;
+  st.a_resident = cnt0 <= 16;
+  g1_load_w_pro(b1, w13, le1, (begin + 1) % D1_NT, kb0, has1);
+  __builtin_amdgcn_sched_barrier(0);
+  dispatch_small_counts_from_masks(T, sh.d);
+  dispatch_small_lists(T, offset, sh.d);
+  if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
   int item = begin;
   if (ring) {
     for (; item + 4 < end; item += 3) {  // items item+2..item+4 exist: unconditional requests

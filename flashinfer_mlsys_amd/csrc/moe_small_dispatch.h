@@ -30,26 +30,52 @@ struct SmallDispatch {
   uint32_t mask[SMALL_T];
 };
 
-// Phase 1 (called by every thread of the workgroup; blockDim.x a multiple of 64
-// and at least SMALL_P; T <= SMALL_T), from the routed ids and weights already
-// in d.ids / d.wts and visible to every thread: one local-expert mask per
-// token, per-expert counts, segment starts and the active list. Enough to know
-// which weights the workgroup will stream.
-__device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, SmallDispatch& d) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+// The phases below are called by every thread of the workgroup (blockDim.x a
+// multiple of 64 and at least SMALL_P; T <= SMALL_T) and synchronise through LDS
+// only (lds_barrier), so loads in flight, such as prefetched weights, are not
+// waited for.
+//
+// Phase 1a, from the routed ids and weights already in d.ids / d.wts and visible
+// to every thread: one local-expert mask per token (bit e: local expert e).
+__device__ __forceinline__ void dispatch_small_masks(int T, int offset, SmallDispatch& d) {
+  const int tid = threadIdx.x;
   if (tid < SMALL_T) d.mask[tid] = 0u;
-  __syncthreads();
+  lds_barrier();
   if (tid < T * TOP_K) {
     const unsigned le = (unsigned)(d.ids[tid] - offset);
     if (le < (unsigned)E_LOCAL) atomicOr(&d.mask[tid >> 3], 1u << le);
     d.pair[tid] = -1;
   }
-  __syncthreads();
+  lds_barrier();
+}
+
+// The active local experts as a bit set, from the token masks (any wave, after
+// dispatch_small_masks; wave-uniform result).
+__device__ __forceinline__ uint32_t small_active_set(int T, const SmallDispatch& d) {
+  const int lane = threadIdx.x & 63;
+  uint32_t m = lane < T ? d.mask[lane] : 0u;
+  m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false);   // lane ^ 1
+  m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false);   // lane ^ 2
+  m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false);  // half-row mirror
+  m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x140, 0xF, 0xF, false);  // row mirror
+  return (uint32_t)__builtin_amdgcn_readlane((int)m, 0) | (uint32_t)__builtin_amdgcn_readlane((int)m, 16) |
+         (uint32_t)__builtin_amdgcn_readlane((int)m, 32) | (uint32_t)__builtin_amdgcn_readlane((int)m, 48);
+}
+
+// Position of the n-th (from 0) set bit of a wave-uniform bit set.
+__device__ __forceinline__ int nth_set_bit(uint32_t set, int n) {
+  for (int j = 0; j < n; ++j) set &= set - 1u;
+  return __builtin_ctz(set);
+}
+
+// Phase 1b: per-expert counts, segment starts and the active list.
+__device__ __forceinline__ void dispatch_small_counts_from_masks(int T, SmallDispatch& d) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   for (int le = wave; le < E_LOCAL; le += nw) {
     const unsigned long long m = __ballot(lane < T && ((d.mask[lane] >> le) & 1u));
     if (lane == 0) d.cnt[le] = __popcll(m);
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {  // segment starts and the active list by one wave: lane e holds expert e
     const int c = lane < E_LOCAL ? d.cnt[lane] : 0;
     int incl = c;  // inclusive prefix sum over lanes
@@ -70,18 +96,28 @@ __device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, Sma
       d.nact = nact;
     }
   }
-  __syncthreads();
+  lds_barrier();
+}
+
+// Phase 1 (1a + 1b): masks, counts, segment starts and the active list. Enough
+// to know which weights the workgroup will stream.
+__device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, SmallDispatch& d) {
+  dispatch_small_masks(T, offset, d);
+  dispatch_small_counts_from_masks(T, d);
 }
 
 // Phase 1 from routed ids and weights in memory.
-__device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                      int T, int offset, SmallDispatch& d) {
+__device__ __forceinline__ void dispatch_small_ids(const int32_t* __restrict__ ids, const float* __restrict__ wts,
+                                                   int T, SmallDispatch& d) {
   const int tid = threadIdx.x;
   if (tid < T * TOP_K) {
     d.ids[tid] = ids[tid];
     d.wts[tid] = wts[tid];
   }
-  __syncthreads();
+}
+__device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
+                                                      int T, int offset, SmallDispatch& d) {
+  dispatch_small_ids(ids, wts, T, d);
   dispatch_small_counts_lds(T, offset, d);
 }
 
@@ -103,7 +139,7 @@ __device__ __forceinline__ void dispatch_small_lists(int T, int offset, SmallDis
       d.pair[lane * TOP_K + slot] = pos;
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 __device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, const float* __restrict__ wts, int T,
