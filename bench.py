@@ -17,7 +17,7 @@ Printed JSON line (rank 0, one line):
   cpu_baseline  the CPU oracle (PyTorch restatement of the reference, all 32 experts
                 dequantised per call as the reference does) timed on this host
   also          the other benchmark configurations (prefill 1024 / 8192, skew 4096) and the
-                producer-side kernels (FP8 activation quantiser, router GEMM) at T = 64 and 8192
+                producer-side kernels (FP8 activation quantiser, router GEMM, both fused) at T = 64 and 8192
 """
 from __future__ import annotations
 
@@ -386,6 +386,23 @@ def main():
             log(f"router_logits T={T}: {us:.1f} us, {rl[f'T={T}']['GB_per_s']} GB/s, "
                 f"{rl[f'T={T}']['TFLOP_per_s']} TFLOP/s")
         also["router_logits"] = rl
+        # both producer steps in one pass over the hidden states
+        rq = {}
+        for T in (64, 8192):
+            x = wl.hidden_bf16(T, 79).to(dev)
+            bufs = (torch.empty((T, wl.E_GLOBAL), dtype=torch.float32, device=dev),
+                    torch.empty((T, wl.H), dtype=torch.float8_e4m3fn, device=dev),
+                    torch.empty((wl.NB_H, T), dtype=torch.float32, device=dev))
+            g = runner.graph(lambda: fm.router_logits_and_quantize(x, gate, out=bufs), args.reps)
+            us = runner.graph_us(g, args.reps)
+            del g
+            nbytes = (T * wl.H * 2 + wl.E_GLOBAL * wl.H * 2 + T * wl.E_GLOBAL * 4
+                      + T * (wl.H + wl.NB_H * 4))
+            rq[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
+                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "separate_us": round(rl[f"T={T}"]["us_per_call"] + qa[f"T={T}"]["us_per_call"], 2)}
+            log(f"router_logits_and_quantize T={T}: {us:.1f} us (separate kernels {rq[f'T={T}']['separate_us']} us)")
+        also["router_logits_and_quantize"] = rq
 
     cpu = None
     if not args.no_cpu_baseline:

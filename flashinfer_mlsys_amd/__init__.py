@@ -26,7 +26,7 @@ import torch
 from . import _lib
 
 __all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_activations", "router_logits",
-           "workspace_size", "MoEInputError", "set_path"]
+           "router_logits_and_quantize", "workspace_size", "MoEInputError", "set_path"]
 
 H = 7168
 I = 2048
@@ -233,6 +233,45 @@ def router_logits(hidden_bf16, gate_weight, out=None):
         code = lib.moe_fp8_router_logits(x.data_ptr(), g.data_ptr(), T, out.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_router_logits")
     return out
+
+
+@torch.no_grad()
+def router_logits_and_quantize(hidden_bf16, gate_weight, out=None):
+    """The producer side (one pass over the bf16 hidden states below 576 tokens,
+    the router and quantiser kernels in turn from 576 on): returns
+    (routing_logits fp32 [T, 256], hidden_states e4m3 [T, 7168], hidden_states_scale
+    fp32 [56, T]), bit for bit what ``router_logits`` and ``quantize_activations``
+    return (reference moe/weight_origins_dataflow.md:19-21, :151-154). ``out`` may
+    pass the three tensors preallocated."""
+    _on_gpu(hidden_bf16, "hidden_bf16")
+    _on_gpu(gate_weight, "gate_weight")
+    _req(hidden_bf16.dtype == torch.bfloat16 and hidden_bf16.dim() == 2 and hidden_bf16.shape[1] == H,
+         "hidden_bf16 must be bf16 [T, 7168]")
+    _req(gate_weight.dtype == torch.bfloat16 and tuple(gate_weight.shape) == (E_GLOBAL, H),
+         "gate_weight must be bf16 [256, 7168]")
+    _req(gate_weight.device == hidden_bf16.device, "gate_weight must be on the hidden states' device")
+    T = hidden_bf16.shape[0]
+    dev = hidden_bf16.device
+    if out is None:
+        logits = torch.empty((T, E_GLOBAL), dtype=torch.float32, device=dev)
+        q = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=dev)
+        scale = torch.empty((H // BLOCK, T), dtype=torch.float32, device=dev)
+    else:
+        logits, q, scale = out
+        _req(logits.dtype == torch.float32 and tuple(logits.shape) == (T, E_GLOBAL) and logits.is_contiguous(),
+             "logits must be a contiguous float32 [T, 256]")
+        _req(q.dtype == torch.float8_e4m3fn and tuple(q.shape) == (T, H) and q.is_contiguous(),
+             "q must be a contiguous float8_e4m3fn [T, 7168]")
+        _req(scale.dtype == torch.float32 and tuple(scale.shape) == (H // BLOCK, T) and scale.is_contiguous(),
+             "scale must be a contiguous float32 [56, T]")
+    if T == 0:
+        return logits, q, scale
+    x, g = _contig(hidden_bf16), _contig(gate_weight)
+    with torch.cuda.device(dev):
+        code = _lib.load().moe_fp8_router_quantize(x.data_ptr(), g.data_ptr(), T, logits.data_ptr(), q.data_ptr(),
+                                                   scale.data_ptr(), _stream(dev))
+    _lib.check(code, "moe_fp8_router_quantize")
+    return logits, q, scale
 
 
 @torch.no_grad()

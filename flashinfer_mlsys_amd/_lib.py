@@ -30,6 +30,7 @@ SIGNATURES = {
     "moe_fp8_route": (ctypes.c_int, [_P, _P, _I64, ctypes.c_double, _P, _P, _P, _P]),
     "moe_fp8_quantize_activations": (ctypes.c_int, [_P, _I64, _P, _P, _P]),
     "moe_fp8_router_logits": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
+    "moe_fp8_router_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "moe_fp8_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "moe_fp8_route_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P, _P, _P, _P, _P]),
     "moe_fp8_set_path": (ctypes.c_int, [ctypes.c_int]),

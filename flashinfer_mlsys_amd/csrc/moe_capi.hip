@@ -19,6 +19,7 @@ hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const
                                int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_quantize_1x128(const uint16_t*, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_router_logits(const uint16_t*, const uint16_t*, int, float*, int, hipStream_t);
+hipError_t launch_router_quantize(const uint16_t*, const uint16_t*, int, float*, uint8_t*, float*, int, hipStream_t);
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const int32_t*,
                                const float*, int, uint16_t*, hipStream_t);
 int gemm1_decode_blocks_per_cu();
@@ -285,6 +286,19 @@ int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weig
   if (!aligned16(hidden_bf16) || !aligned16(gate_weight) || !aligned16(routing_logits)) return MOE_ERR_ALIGN;
   hipError_t e = moe::launch_router_logits(hidden_bf16, gate_weight, (int)T, routing_logits, cu_count(),
                                            reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MOE_OK : hip_fail(e);
+}
+
+int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
+                            float* routing_logits, uint8_t* hidden_states, float* hidden_states_scale, void* stream) {
+  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T == 0) return MOE_OK;
+  if (!hidden_bf16 || !gate_weight || !routing_logits || !hidden_states || !hidden_states_scale) return MOE_ERR_NULL;
+  if (!aligned16(hidden_bf16) || !aligned16(gate_weight) || !aligned16(routing_logits) || !aligned16(hidden_states) ||
+      !aligned16(hidden_states_scale))
+    return MOE_ERR_ALIGN;
+  hipError_t e = moe::launch_router_quantize(hidden_bf16, gate_weight, (int)T, routing_logits, hidden_states,
+                                             hidden_states_scale, cu_count(), reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 

@@ -16,7 +16,7 @@
 // tokens 4w..4w+3, 16 lanes per (token, block), each lane 8 elements (16 B in,
 // 8 B out). The 4 scales a wave writes per block are 4 consecutive floats of
 // the transposed scale array.
-#include "moe_common.h"
+#include "moe_quant_block.h"
 
 namespace moe {
 
@@ -39,31 +39,17 @@ __global__ __launch_bounds__(256) void quantize_1x128_kernel(const uint16_t* __r
     if (valid) {
       const uint4 raw = *reinterpret_cast<const uint4*>(xr + kb * BLK);
       const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
+      bf16x8_to_f32(w, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     }
     // block max over the 16 lanes of this (token, block)
 #pragma unroll
     for (int k = 1; k < 16; k <<= 1) m = fmaxf(m, __shfl_xor(m, k));
-    const float s = fmaxf(m, 1e-12f) / 448.0f;
+    const float s = qblock_scale(m);
     if (valid) {
-      uint32_t packed[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const float a = fminf(fmaxf(v[4 * i] / s, -448.f), 448.f);
-        const float b = fminf(fmaxf(v[4 * i + 1] / s, -448.f), 448.f);
-        const float c = fminf(fmaxf(v[4 * i + 2] / s, -448.f), 448.f);
-        const float d = fminf(fmaxf(v[4 * i + 3] / s, -448.f), 448.f);
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, 0, false) & 0xffffu;
-        packed[i] = lo | (hi << 16);
-      }
-      *reinterpret_cast<uint2*>(qr + kb * BLK) = uint2{packed[0], packed[1]};
+      const uint32_t p0 = qblock_pack4(v[0], v[1], v[2], v[3], s), p1 = qblock_pack4(v[4], v[5], v[6], v[7], s);
+      *reinterpret_cast<uint2*>(qr + kb * BLK) = uint2{p0, p1};
       if (r == 0) scale[(size_t)kb * T + t] = s;
     }
   }

@@ -10,12 +10,23 @@
 // then the 8 partial tiles are added through LDS in wave order (deterministic, no
 // atomics, no workspace).
 //
+// With QUANT the small-T kernel also writes the operator's FP8 activation inputs
+// (e4m3 rows [T, 7168] and 1 x 128 block scales [56, T]) from the hidden states
+// it reads anyway, with the quantiser kernel's arithmetic, each (token, K block)
+// exactly once: the workgroup of expert tile y quantises the K blocks kb with
+// kb % 16 == y from the fragments it holds (one pass over x instead of two:
+// 15 us instead of 20 at T=64). From RT2_MIN_T tokens on the two producer steps
+// run as the tiled kernel and the quantiser kernel: the same quantisation inside
+// the tiled kernel's compute waves (2 per SIMD, next to the loader waves) cost
+// more than the separate quantiser (84 against 49 + 40 us at T=8192).
+//
 // Larger T: LDS-staged tiles of 128 tokens x 64 experts, 8 compute waves of
 // 32 x 32 (v_mfma_f32_32x32x16_bf16) and 4 loader waves that stream each 128-wide
 // K block (hidden rows and gate rows, whole 128 B lines, 32-row swizzle) into a
 // 3-slot LDS ring two blocks ahead, as the prefill GEMM1 does.
 #include "moe_common.h"
 #include "moe_tile.h"
+#include "moe_quant_block.h"
 
 namespace moe {
 
@@ -28,9 +39,11 @@ __device__ __forceinline__ v8bf load_bf16x8(const uint16_t* p) {
 constexpr int RS_WAVES = 8;
 constexpr int RS_KPW = NB_H / RS_WAVES;  // 7 K blocks per wave
 
+template <bool QUANT>
 __global__ __launch_bounds__(64 * RS_WAVES) void router_small_kernel(const uint16_t* __restrict__ x,
                                                                      const uint16_t* __restrict__ g, int T,
-                                                                     float* __restrict__ logits) {
+                                                                     float* __restrict__ logits, uint8_t* __restrict__ q,
+                                                                     float* __restrict__ qs) {
   __shared__ float red[RS_WAVES][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int fr = lane & 15, kg = lane >> 4;
@@ -54,6 +67,38 @@ __global__ __launch_bounds__(64 * RS_WAVES) void router_small_kernel(const uint1
     for (int s = 0; s < 4; ++s) acc = mfma_bf16_k32(a[kk][s], b[kk][s], acc);
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+  if (QUANT) {
+    // lane (fr, kg) holds K 32 s + 8 kg + [0, 8) of token row fr for s = 0..3; the
+    // row's 4 lanes are fr, fr + 16, fr + 32, fr + 48
+    const int t = t0 + fr;
+#pragma unroll
+    for (int kk = 0; kk < RS_KPW; ++kk) {
+      const int kb = wave * RS_KPW + kk;
+      if (kb % 16 != (int)blockIdx.y) continue;  // wave-uniform
+      float v[4][8];
+      float m = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const v4i w = __builtin_bit_cast(v4i, a[kk][s4]);
+        const uint32_t wu[4] = {(uint32_t)w[0], (uint32_t)w[1], (uint32_t)w[2], (uint32_t)w[3]};
+        bf16x8_to_f32(wu, v[s4]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[s4][i]));
+      }
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      const float sc = qblock_scale(m);
+      if (t < T) {
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const uint32_t p0 = qblock_pack4(v[s4][0], v[s4][1], v[s4][2], v[s4][3], sc);
+          const uint32_t p1 = qblock_pack4(v[s4][4], v[s4][5], v[s4][6], v[s4][7], sc);
+          *reinterpret_cast<uint2*>(q + (size_t)t * H + kb * BLK + 32 * s4 + 8 * kg) = uint2{p0, p1};
+        }
+        if (kg == 0) qs[(size_t)kb * T + t] = sc;
+      }
+    }
+  }
   __syncthreads();
   if (threadIdx.x < 256) {  // entry (r, lane): token row 4 (lane / 16) + r, expert column lane % 16
     const int r = threadIdx.x >> 6, ln = threadIdx.x & 63;
@@ -176,25 +221,42 @@ __global__ __launch_bounds__(64 * (RT2_CWAVES + RT2_PWAVES), 1) void router_tile
   }
 }
 
+hipError_t launch_quantize_1x128(const uint16_t* x, int T, uint8_t* q, float* scale, hipStream_t stream);
+
+static hipError_t launch_router_tiled(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
+                                      hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tiled_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, RT2_NSTAGE * RT2_STAGE);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int items = (T + RT2_BM - 1) / RT2_BM * RT2_NT;
+  const int grid = min((items + 7) / 8 * 8, (cu + 7) / 8 * 8);
+  hipLaunchKernelGGL(router_tiled_kernel, dim3(grid), dim3(64 * (RT2_CWAVES + RT2_PWAVES)), RT2_NSTAGE * RT2_STAGE,
+                     stream, x, g, T, logits);
+  return hipGetLastError();
+}
+
 hipError_t launch_router_logits(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
                                 hipStream_t stream) {
   if (T <= 0) return hipSuccess;
+  if (T >= RT2_MIN_T) return launch_router_tiled(x, g, T, logits, cu, stream);
+  hipLaunchKernelGGL(router_small_kernel<false>, dim3((T + RT_M - 1) / RT_M, E_GLOBAL / 16), dim3(64 * RS_WAVES), 0,
+                     stream, x, g, T, logits, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_quantize(const uint16_t* x, const uint16_t* g, int T, float* logits, uint8_t* q, float* qs,
+                                  int cu, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
   if (T >= RT2_MIN_T) {
-    static bool attr_set = false;
-    if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tiled_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, RT2_NSTAGE * RT2_STAGE);
-      if (e != hipSuccess) return e;
-      attr_set = true;
-    }
-    const int items = (T + RT2_BM - 1) / RT2_BM * RT2_NT;
-    const int grid = min((items + 7) / 8 * 8, (cu + 7) / 8 * 8);
-    hipLaunchKernelGGL(router_tiled_kernel, dim3(grid), dim3(64 * (RT2_CWAVES + RT2_PWAVES)),
-                       RT2_NSTAGE * RT2_STAGE, stream, x, g, T, logits);
-    return hipGetLastError();
+    const hipError_t e = launch_router_tiled(x, g, T, logits, cu, stream);
+    return e != hipSuccess ? e : launch_quantize_1x128(x, T, q, qs, stream);
   }
-  hipLaunchKernelGGL(router_small_kernel, dim3((T + RT_M - 1) / RT_M, E_GLOBAL / 16), dim3(64 * RS_WAVES), 0, stream,
-                     x, g, T, logits);
+  hipLaunchKernelGGL(router_small_kernel<true>, dim3((T + RT_M - 1) / RT_M, E_GLOBAL / 16), dim3(64 * RS_WAVES), 0,
+                     stream, x, g, T, logits, q, qs);
   return hipGetLastError();
 }
 

@@ -144,6 +144,18 @@ int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t
 int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
                           float* routing_logits, void* stream);
 
+/*
+ * Both producer-side steps (the router GEMM of moe_fp8_router_logits and the
+ * quantiser of moe_fp8_quantize_activations, reference
+ * moe/weight_origins_dataflow.md:19-21 and :21, :151-154, which read the same
+ * x): one pass over the bf16 hidden states below 576 tokens, the two kernels
+ * in turn from 576 on; writes the same routing_logits, hidden_states and
+ * hidden_states_scale, bit for bit, as the two separate calls. All pointers
+ * 16-byte aligned. Stream-ordered.
+ */
+int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
+                            float* routing_logits, uint8_t* hidden_states, float* hidden_states_scale, void* stream);
+
 /* Kernel shape used by moe_fp8_forward: 0 = by token count (default: the
  * decode shape for T <= 64, the prefill shape above), 1 = the same as 0
  * (the decode shape exists only for T <= 64), 2 = always the prefill shape.

@@ -108,6 +108,19 @@ def test_router_argument_errors(lib):
     assert r(FAKE, FAKE, 4, FAKE + 4, None) == _lib.MOE_ERR_ALIGN
 
 
+def test_router_quantize_argument_errors(lib):
+    r = lib.moe_fp8_router_quantize
+    assert r(FAKE, FAKE, 0, None, None, None, None) == _lib.MOE_OK  # nothing to do, nothing read
+    assert r(FAKE, FAKE, -1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, (1 << 20) + 1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    for i in range(5):
+        args = [FAKE] * 5
+        args[i] = None
+        assert r(args[0], args[1], 4, args[2], args[3], args[4], None) == _lib.MOE_ERR_NULL, i
+        args[i] = FAKE + 4
+        assert r(args[0], args[1], 4, args[2], args[3], args[4], None) == _lib.MOE_ERR_ALIGN, i
+
+
 def test_set_path(lib):
     assert lib.moe_fp8_set_path(7) == -1
     old = lib.moe_fp8_set_path(2)

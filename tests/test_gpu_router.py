@@ -64,6 +64,23 @@ def test_router_deterministic_and_in_place(dev, gate, T):
     assert b is out and torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T", [1, 5, 16, 17, 64, 100, 575, 576, 1024, 3000])
+def test_fused_producer_equals_separate_kernels(dev, gate, T):
+    """router_logits_and_quantize writes the same logits, e4m3 rows and scales, bit
+    for bit, as router_logits and quantize_activations (both kernels' tilings, ragged
+    tiles); the rows and scales also equal the CPU oracle's quantiser."""
+    print(f"fused producer T={T}", flush=True)
+    x = wl.hidden_bf16(T, 300 + T)
+    xd = x.to(dev)
+    lg, q, s = fm.router_logits_and_quantize(xd, gate[1])
+    assert torch.equal(lg, fm.router_logits(xd, gate[1]))
+    q2, s2 = fm.quantize_activations(xd)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+    if T <= 100:
+        qr, sr = cpu_ref.quantize_activations(x)
+        assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s.cpu(), sr)
+
+
 # (T, local_expert_offset, seed): the first seed from 9000 + T whose oracle-chain
 # selection margins are at least 256 fp32 ulps (the GPU logits differ from the CPU's
 # fp32 matmul by summation order, far below that) and that routes a local pair.
