@@ -1,7 +1,8 @@
 // extern "C" boundary of libmoe_mi355x.so (declarations and contract in
 // include/moe_fp8.h). Validates arguments, carves the workspace and enqueues
 // the kernels on the caller's stream: route -> dispatch -> GEMM1+SwiGLU ->
-// GEMM2 x weight -> ordered combine. No host synchronisation, no allocation.
+// GEMM2 x weight -> ordered combine (inside GEMM2 in the decode shape). No host
+// synchronisation, no allocation.
 #include "moe_common.h"
 #include "../../include/moe_fp8.h"
 

@@ -4,8 +4,9 @@
 //   GEMM1  G1 = A_e . W13_e^T        [cnt, 7168] x [7168, 4096]  (ref_moe.py:147-153)
 //   SwiGLU C  = X1 * silu(X2)        X1 = G1[:, :2048], X2 = G1[:, 2048:] (ref_moe.py:155-159)
 //   GEMM2  O  = C . W2_e^T           [cnt, 2048] x [2048, 7168]  (ref_moe.py:161-162)
-//   weight O * w[token, e] into one fp32 row per (token, expert) pair
-//   combine: out[t] = sum over t's local experts in ascending id, then bf16 (ref_moe.py:164-168)
+//   weight O * w[token, e]; out[t] = sum over t's local experts in ascending id,
+//   then bf16 (ref_moe.py:164-168): in the decode shape inside GEMM2, in the
+//   prefill shape through one fp32 row per (token, expert) pair and the combine
 //
 // GEMM1 runs on the e4m3 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
 // scales). One MFMA covers exactly one 128-wide K block, so the fp32 block
@@ -14,17 +15,20 @@
 // keeps the SwiGLU output to 8 significant bits.
 //
 // Two shapes of each GEMM:
-//   *_decode  -- T <= 64, few rows per expert, weight-streaming bound.
-//                Persistent workgroups walk (active expert, column tile) items;
-//                the waves split K, so each weight byte is read once, and the
-//                next item's weights are in flight while the current one
-//                computes. Partial sums meet in LDS; GEMM2 also does the combine.
-//   *_tiled   -- many rows per expert (prefill). Persistent workgroups walk a
+//   *_decode  -- T <= 64, few rows per expert, weight-streaming bound. The
+//                waves split K, so each weight byte is read once, and the next
+//                items' weights are in flight while the current one computes;
+//                partial sums meet in LDS. GEMM1: persistent workgroups walk
+//                (active expert, 8-column) items. GEMM2: workgroup c owns 28
+//                output columns of every active expert and sums each token's
+//                pairs itself, writing bf16 rows (no combine kernel).
+//   *_loader  -- many rows per expert (prefill). Persistent workgroups walk a
 //                device-built list of (expert, row tile, column tile) items;
-//                operands go global -> LDS with direct loads into a ring of
-//                stages, in the exact order the MFMA reads them. The workgroups
-//                of one XCD take consecutive items, which share the weight tile,
-//                so that XCD's L2 serves the repeats.
+//                loader waves move operands global -> LDS with direct loads into
+//                a ring of stages, in the exact order the MFMA reads them, while
+//                compute waves run the MFMAs. The workgroups of one XCD take
+//                consecutive items, which share the weight tile, so that XCD's
+//                L2 serves the repeats.
 #include "moe_common.h"
 #include "moe_route_token.h"
 #include "moe_small_dispatch.h"
