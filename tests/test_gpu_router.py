@@ -81,6 +81,29 @@ def test_fused_producer_equals_separate_kernels(dev, gate, T):
         assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s.cpu(), sr)
 
 
+@pytest.mark.parametrize("T", [37, 700])
+def test_producer_graph_replay(dev, gate, T):
+    """The producer step (fused below 576 tokens, two kernels from 576) captured in a
+    HIP graph: each replay, with eager work in between, reproduces the eager result."""
+    x = wl.hidden_bf16(T, 41).to(dev)
+    bufs = (torch.empty((T, 256), device=dev), torch.empty((T, 7168), dtype=torch.float8_e4m3fn, device=dev),
+            torch.empty((56, T), device=dev))
+    fm.router_logits_and_quantize(x, gate[1], out=bufs)
+    torch.cuda.synchronize()
+    ref = [b.clone() for b in bufs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fm.router_logits_and_quantize(x, gate[1], out=bufs)
+    for i in range(3):
+        for b in bufs:
+            b.view(torch.uint8).fill_(0x55)
+        fm.router_logits(wl.hidden_bf16(16, 6).to(dev), gate[1])  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for b, r in zip(bufs, ref):
+            assert torch.equal(b.view(torch.uint8), r.view(torch.uint8)), f"replay {i}"
+
+
 # (T, local_expert_offset, seed): the first seed from 9000 + T whose oracle-chain
 # selection margins are at least 256 fp32 ulps (the GPU logits differ from the CPU's
 # fp32 matmul by summation order, far below that) and that routes a local pair.
