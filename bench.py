@@ -218,6 +218,26 @@ def traffic_pass(dev, weights_gpu, sweep, reps):
                       round(statistics.fmean(c.gemm1_bytes for c in cases))}), flush=True)
 
 
+MFMA_PASS_CASES = ("prefill_t8192", "skew_t4096")
+
+
+def mfma_pass(dev, weights_gpu, reps):
+    """Launches for the MFMA counters (SQ_VALU_MFMA_BUSY_CYCLES with GRBM_GUI_ACTIVE,
+    SQ_INSTS_VALU_MFMA_MOPS_F8 / _BF16): `reps` operator calls of each large prefill
+    configuration in turn, so the prefill GEMM kernels' dispatches come in that order."""
+    cases = [Case(n, dev, weights_gpu) for n in MFMA_PASS_CASES]
+    runner = Runner(dev, max(c.T for c in cases))
+    info = []
+    for c in cases:
+        for _ in range(reps):
+            runner.call(c)
+        torch.cuda.synchronize()
+        log(f"{c.name}: {reps} calls done")
+        info.append({"name": c.name, "T": c.T, "P": c.P, "E_act": c.E_act, "calls": reps,
+                     "gemm1_flop": c.P * 2 * (2 * wl.I) * wl.H, "gemm2_flop": c.P * 2 * wl.H * wl.I})
+    print(json.dumps({"mfma_pass": True, "cases": info}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -229,6 +249,9 @@ def main():
     ap.add_argument("--traffic-pass", action="store_true",
                     help="only run the launches a rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE pass reads: a copy "
                          "kernel of known size, then --reps operator calls at each T of the sweep")
+    ap.add_argument("--mfma-pass", action="store_true",
+                    help="only run the launches a rocprofv3 --pmc MFMA pass reads: --reps operator calls of "
+                         "the T=8192 prefill and the skewed T=4096 configurations")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -247,6 +270,9 @@ def main():
     sweep = list(wl.DECODE_SWEEP)
     if args.traffic_pass:
         traffic_pass(dev, weights_gpu, sweep, args.reps)
+        return
+    if args.mfma_pass:
+        mfma_pass(dev, weights_gpu, args.reps)
         return
     extra = [] if args.no_extra else ["t16", "prefill_t1024", "prefill_t8192", "skew_t4096"]
     cases = {n: Case(n, dev, weights_gpu) for n in sweep + extra}
