@@ -619,62 +619,190 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
 
 
 // ---------------------------------------------------------------------------
-// Shared item list for the tiled kernels: every workgroup rebuilds the
-// per-expert row-tile prefix from the dispatch header (32 values).
+// Items of the tiled (prefill) kernels: (row tile, column tile) pairs.
+//
+// Row tiles are BM = 128 rows of one expert's segment, numbered expert by
+// expert in descending order of the experts' row counts (ties: lower id first),
+// each expert's tiles in row order. All tiles of an expert share its weight
+// tiles, which stay in the caches while they run; the largest experts (whose
+// tiles are full and cost the most: the compute waves skip row fragments past
+// the valid count) come first, and the one-tile experts with few rows, the
+// cheapest items, last, where they even out the workgroups' finishing times.
+// The block order: blocks of 8 row tiles x 4 column tiles, row-block major.
+//
+// GEMM1 deals the block order statically in rounds (snake_item): each 32-item
+// block runs on the 32 workgroups of one XCD in step, sharing its 8 activation
+// and 4 weight tiles in that XCD's L2. (Handing its items out at run time, as
+// GEMM2 does, was measured slower: the workgroups of an XCD drift apart and
+// the L2 stops serving the repeats.)
+//
+// GEMM2 hands its items out at run time: the blocks are dealt round robin to 8
+// queues, one per XCD (hardware places workgroup b on XCD b % 8, which only
+// matters for cache locality: correctness never depends on it); the
+// workgroups of an XCD take the items of its queue in order with an atomic
+// position counter, and a workgroup whose queue is empty takes from the next
+// queues in turn. The last workgroup to find every queue empty resets the
+// counters for the next launch (the dispatch kernel zeroes them too, with the
+// rest of the header).
 // ---------------------------------------------------------------------------
+constexpr int TB_M = 8, TB_N = 4, N_XCD = 8;
+static_assert(NB_I >= 6 && NB_H >= 6, "the item feed needs K blocks 0 .. 3 and two more");
+
 struct TileMap {
-  int mt_prefix[E_LOCAL + 1];
-  int cnt[E_LOCAL];
+  int order[E_LOCAL];     // expert of each rank (descending row count)
+  int pref[E_LOCAL + 1];  // first row tile of each rank
+  int cnt[E_LOCAL];       // by expert id
   int seg[E_LOCAL];
+  int total_m;            // row tiles
+  int ring[4];            // item of sequence number s at ring[s % 4] (-1: no more)
 };
 
 template <int BM>
 __device__ __forceinline__ void build_tile_map(const DispatchHeader* hdr, TileMap& m) {
   const int tid = threadIdx.x;
-  if (tid < E_LOCAL) {
-    m.cnt[tid] = hdr->counts[tid];
-    m.seg[tid] = hdr->seg_start[tid];
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int e = 0; e < E_LOCAL; ++e) {
-      m.mt_prefix[e] = acc;
-      acc += (m.cnt[e] + BM - 1) / BM;
+  if (tid < 64) {
+    const int lane = tid;
+    const int cnt = lane < E_LOCAL ? hdr->counts[lane] : -1;
+    const int seg = lane < E_LOCAL ? hdr->seg_start[lane] : 0;
+    int rank = 0;  // experts before this one: more rows, or as many and a lower id
+    for (int j = 0; j < E_LOCAL; ++j) {
+      const int cj = __shfl(cnt, j);
+      rank += (cj > cnt || (cj == cnt && j < lane)) ? 1 : 0;
     }
-    m.mt_prefix[E_LOCAL] = acc;
+    if (lane < E_LOCAL) {
+      m.cnt[lane] = cnt;
+      m.seg[lane] = seg;
+      m.order[rank] = lane;
+    }
+    // tiles by rank: this wave wrote order[] and reads it back (its own LDS
+    // accesses stay in order)
+    const int e = lane < E_LOCAL ? m.order[lane] : 0;
+    int inc = lane < E_LOCAL ? (__shfl(cnt, e) + BM - 1) / BM : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(inc, d);
+      if (lane >= d) inc += o;
+    }
+    if (lane < E_LOCAL) m.pref[lane + 1] = inc;
+    if (lane == 0) m.pref[0] = 0;
+    if (lane == E_LOCAL - 1) m.total_m = inc;
   }
   __syncthreads();
 }
 
-// Item order for the tiled kernels: blocks of 8 row tiles x 4 column tiles.
-// With xcd_remap the 32 workgroups of one XCD take one block per round (on a
-// 256-CU part), so the concurrently streamed K blocks of 8 activation tiles
-// and 4 weight tiles are shared in that XCD's L2 (8 + 4 distinct tiles instead
-// of 32 + 1 for a column-tile-major order). Blocks run row-block major, all
-// column blocks of a row block back to back. Row tiles past total_m are empty
-// items (the caller skips them).
-constexpr int TB_M = 8, TB_N = 4;
-__device__ __forceinline__ int tiled_items(int total_m, int nt_count) {
-  return (total_m + TB_M - 1) / TB_M * TB_M * nt_count;
-}
-__device__ __forceinline__ void tiled_item_coords(int item, int nt_count, int& mg, int& nt) {
-  const int blk = item / (TB_M * TB_N), i = item % (TB_M * TB_N);
-  const int nbk = nt_count / TB_N;
-  mg = (blk / nbk) * TB_M + i % TB_M;
-  nt = (blk % nbk) * TB_N + i / TB_M;
+// Row tile k -> its expert and first row within the expert's segment.
+template <int BM>
+__device__ __forceinline__ void tile_row(const TileMap& m, int k, int& e, int& m0) {
+  int j = 0;
+  while (m.pref[j + 1] <= k) ++j;
+  e = m.order[j];
+  m0 = (k - m.pref[j]) * BM;
 }
 
-__device__ __forceinline__ int find_expert(const TileMap& m, int mg) {
-  int e = 0;
-  while (m.mt_prefix[e + 1] <= mg) ++e;
-  return e;
+// Length of queue x: the blocks b = x + 8 j; only the blocks of the last row
+// block hold fewer than 32 items, and each queue holds at most one of them (its last).
+__device__ __forceinline__ int queue_len(int x, int total_m, int nbk) {
+  const int nrb = (total_m + TB_M - 1) / TB_M, nblocks = nrb * nbk;
+  if (x >= nblocks) return 0;
+  const int nj = (nblocks - x + N_XCD - 1) / N_XCD;
+  const int last = x + N_XCD * (nj - 1);
+  const int rows_last = total_m - TB_M * (nrb - 1);
+  return TB_M * TB_N * nj - (last / nbk == nrb - 1 ? (TB_M - rows_last) * TB_N : 0);
 }
+
+// Position q < queue_len(x) of queue x -> item id k * (4 nbk) + nt.
+__device__ __forceinline__ int queue_item(int x, int q, int total_m, int nbk) {
+  const int nrb = (total_m + TB_M - 1) / TB_M;
+  const int b = x + N_XCD * (q / (TB_M * TB_N)), i = q % (TB_M * TB_N);
+  const int rb = b / nbk, cb = b % nbk;
+  const int rows = rb == nrb - 1 ? total_m - TB_M * rb : TB_M;
+  return (TB_M * rb + i % rows) * (TB_N * nbk) + TB_N * cb + i / rows;
+}
+
+// The static deal (GEMM1): item i of the block order (all blocks row-block
+// major, the last row block's blocks shorter) -> item id k * nt_count + nt.
+__device__ __forceinline__ int block_order_item(int i, int total_m, int nt_count) {
+  const int nbk = nt_count / TB_N, nrb = (total_m + TB_M - 1) / TB_M;
+  const int full = (nrb - 1) * nbk * TB_M * TB_N;
+  int rb, cb, ii, rows;
+  if (i < full) {
+    const int b = i / (TB_M * TB_N);
+    rb = b / nbk;
+    cb = b % nbk;
+    ii = i % (TB_M * TB_N);
+    rows = TB_M;
+  } else {
+    rows = total_m - TB_M * (nrb - 1);
+    rb = nrb - 1;
+    cb = (i - full) / (rows * TB_N);
+    ii = (i - full) % (rows * TB_N);
+  }
+  return (TB_M * rb + ii % rows) * nt_count + TB_N * cb + ii / rows;
+}
+// Round r of the G workgroups takes items r G .. r G + G - 1 of the block
+// order: slot p (xcd_remap: the G / 8 slots of an XCD are consecutive, so each
+// 32-item block runs on one XCD with its workgroups in step, sharing the
+// block's operand tiles in its L2) takes item r G + p in even rounds and
+// r G + G - 1 - p in odd ones, so that the slots that took the cheaper items of
+// one round take the costlier ones of the next.
+__device__ __forceinline__ int snake_item(int r, int slot, int G) { return r * G + ((r & 1) ? G - 1 - slot : slot); }
+
+// The workgroup's item source, used by one lane: pos[8] and done live in the
+// dispatch header.
+struct ItemQueue {
+  int* pos;
+  int* done;
+  int home, x, total_m, nbk;
+
+  __device__ __forceinline__ void init(int* pos_, int* done_, int total_m_, int nt_count) {
+    pos = pos_;
+    done = done_;
+    home = x = blockIdx.x % N_XCD;
+    total_m = total_m_;
+    nbk = nt_count / TB_N;
+  }
+  __device__ __forceinline__ int len(int qx) const { return queue_len(qx, total_m, nbk); }
+  __device__ __forceinline__ int item(int qx, int q) const { return queue_item(qx, q, total_m, nbk); }
+  // The item at position q of queue x if that exists, else the next item from the
+  // following queues in turn; -1 once every queue is empty (and then the
+  // workgroup counts itself out, the last one resetting the counters; the
+  // caller asks no more).
+  __device__ int resolve(int q) {
+    for (;;) {
+      if (q < len(x)) return item(x, q);
+      x = (x + 1) % N_XCD;
+      if (x == home) break;
+      q = atomicAdd(&pos[x], 1);
+    }
+    if (atomicAdd(done, 1) == (int)gridDim.x - 1) {
+      for (int i = 0; i < N_XCD; ++i) atomicExch(&pos[i], 0);
+      atomicExch(done, 0);
+    }
+    return -1;
+  }
+  __device__ __forceinline__ int ask() { return atomicAdd(&pos[x], 1); }
+};
+
+// Lane 0 of the last loader wave keeps the item ring one item ahead: right
+// after issuing K block 0 of an item it asks for the next position, and before
+// issuing K block FEED_KB it resolves the answer and writes the ring entry
+// (the atomic has had a few K blocks to return; every wave reads the entry at
+// least one barrier later: the loader waves when they start the next item, the
+// compute waves after finishing this one). It lives in a loader wave so that
+// its state takes no registers from the compute waves' MFMA loop.
+constexpr int FEED_KB = 3;
+struct ItemFeed {
+  ItemQueue q;
+  int pending;
+  __device__ __forceinline__ void ask() { pending = q.ask(); }
+  __device__ __forceinline__ int resolve() { return q.resolve(pending); }
+};
 
 // ---------------------------------------------------------------------------
 // GEMM1 + SwiGLU, prefill shape: 128 rows x 128 column pairs (X1 rows n..n+127
 // and X2 rows 2048+n..) per item. 8 compute waves as 2 (rows) x 4 (pairs); each
-// owns 64 rows x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles), and 4
+// owns 64 rows (the 16-row fragments 2 mt + wm, mt < 4, so the two row halves
+// interleave) x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles), and 4
 // loader waves move the operands.
 //
 // Operands go global -> LDS with the direct load (global_load_lds_dwordx4):
@@ -740,57 +868,103 @@ __device__ __forceinline__ int spread_lanes(const int (&t)[32], int base) {
   return v;
 }
 
+// One item's 56 K blocks for a compute wave of the GEMM1 loader kernel: NMT of
+// its 16-row fragments (2 mt + wm, mt < NMT) against its 2 X1 and 2 X2 column
+// tiles. Fragments past the item's valid rows are skipped (their rows would be
+// discarded), so a partly filled tile costs MFMA and scale work in proportion
+// to its rows; the interleaved fragment order keeps the two row halves' waves,
+// which sit on different SIMDs, within one fragment of each other. Every wave
+// takes the barrier of every K block whatever its NMT.
+template <int NMT>
+__device__ __forceinline__ void g1_loader_kloop(const uint8_t* q1_lds, int& slot, int wm, int wn, int kg, int flo,
+                                                int fhi, v4f (&accu)[4][2], v4f (&accg)[4][2]) {
+#pragma unroll 1
+  for (int kb = 0; kb < NB_H; ++kb) {
+    __builtin_amdgcn_s_barrier();  // K block kb is in its slot; the slot before it is free
+    asm volatile("" ::: "memory");
+    const uint8_t* st = q1_lds + slot * W1_STAGE;
+    slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
+    if constexpr (NMT > 0) {
+      v8i a[NMT];
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) a[mt] = lds_frag_sw(st + (2 * mt + wm) * FRAG_BYTES, flo, fhi);
+      v4f pu[NMT][2], pg[NMT][2];
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2) {
+        const v8i bu = lds_frag_sw(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
+        const v8i bg = lds_frag_sw(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) {
+          pu[mt][n2] = mfma_fp8_k128(a[mt], bu);
+          pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
+        }
+      }
+      const float swu = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF);
+      const float swg = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF + 4);
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
+        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + ((2 * mt + wm) * 16 + 4 * kg) * 4);
+        v4f fu, fg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
+#pragma unroll
+        for (int n2 = 0; n2 < 2; ++n2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
+            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
+          }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+  }
+}
+
 __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, DispatchHeader* __restrict__ hdr,
     const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q1_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   build_tile_map<Q1_BM>(hdr, map);
-  const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = tiled_items(total_m, Q1_NT);
-  const int first = xcd_remap(blockIdx.x, gridDim.x);
-  int n_items = 0;
-  for (int item = first; item < total; item += gridDim.x) {
-    int mg, nt;
-    tiled_item_coords(item, Q1_NT, mg, nt);
-    n_items += mg < total_m;
-  }
-  const int G = n_items * NB_H;  // K blocks this workgroup runs, over all its items
+  const int total = map.total_m * Q1_NT, G = gridDim.x;
+  const int my_slot = xcd_remap(blockIdx.x, G);
 
   if (wave >= W1_CWAVES) {
     // ----------------------------- loader waves -----------------------------
     const int p = wave - W1_CWAVES, rr = lane >> 3;
     // the tile map in registers (lane e < 32 holds expert e's values), read before any
     // direct load is in flight: later LDS reads would wait for every load in flight
-    const int my_pref = lane < E_LOCAL ? map.mt_prefix[lane] : 0;
-    const int my_next = lane < E_LOCAL ? map.mt_prefix[lane + 1] : 0x7fffffff;
+    const int my_pref = lane < E_LOCAL ? map.pref[lane] : 0;
+    const int my_next = lane < E_LOCAL ? map.pref[lane + 1] : 0x7fffffff;
+    const int my_order = lane < E_LOCAL ? map.order[lane] : 0;
     const int my_cnt = lane < E_LOCAL ? map.cnt[lane] : 0;
     const int my_seg = lane < E_LOCAL ? map.seg[lane] : 0;
+    const int map_total_m = map.total_m;
     const uint8_t* srcA[W1_AJOBS];
     const uint8_t* srcB[W1_BJOBS];
     const float* ssrc = hscale;
     int sstride = T;
     const bool scale_lane = lane < 32 || (p == W1_PWAVES - 1 && lane < 34);
-    int item = first - (int)gridDim.x, kb = NB_H, slot = 0;
+    int round = -1, kb = NB_H, slot = 0, issued = 0;
+    bool more = true;
 
-    auto next_item = [&]() {
-      int mg = 0, nt = 0;
-      for (item += gridDim.x; item < total; item += gridDim.x) {
-        tiled_item_coords(item, Q1_NT, mg, nt);
-        if (mg < total_m) break;
-      }
-      if (item >= total) return;
-      const int e = __popcll(__ballot(my_next <= mg));  // experts whose tiles all lie before mg
+    auto next_item = [&]() -> bool {
+      const int i = snake_item(++round, my_slot, G);
+      if (i >= total) return false;
+      const int it = block_order_item(i, map_total_m, Q1_NT);
+      const int k = it / Q1_NT, nt = it % Q1_NT;
+      const int j = __popcll(__ballot(my_next <= k));  // ranks whose tiles all lie before k
+      const int e = __builtin_amdgcn_readlane(my_order, j);
+      const int m0 = (k - __builtin_amdgcn_readlane(my_pref, j)) * Q1_BM;
       const int cnt = __builtin_amdgcn_readlane(my_cnt, e), seg = __builtin_amdgcn_readlane(my_seg, e);
-      const int m0 = (mg - __builtin_amdgcn_readlane(my_pref, e)) * Q1_BM;
       const int valid = min(Q1_BM, cnt - m0);
       const int32_t* tp = perm_tok + seg + m0;
       int tk[32];
 #pragma unroll
-      for (int k = 0; k < 32; ++k) tk[k] = tp[32 * p + k];
+      for (int j = 0; j < 32; ++j) tk[j] = tp[32 * p + j];
       const int tok0 = tp[0];
       // every spread first, with all lanes active (see spread_lanes), then the
       // per-lane choice: rows at or past the valid count take the first token
@@ -818,9 +992,10 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
         sstride = 1;
       }
       kb = 0;
+      return true;
     };
     auto issue = [&]() {
-      if (kb == NB_H) next_item();
+      if (kb == NB_H && !(more = next_item())) return;
       uint8_t* st = q1_lds + slot * W1_STAGE;
 #pragma unroll
       for (int i = 0; i < W1_AJOBS; ++i)
@@ -832,16 +1007,17 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
       if (scale_lane) lds_direct4(ssrc + (size_t)kb * sstride, st + Q1_SCALE_OFF + 128 * p);
       slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
       ++kb;
+      ++issued;
     };
-    if (G > 0) issue();
-    if (G > 1) issue();
+    issue();
+    if (more) issue();
 #pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-      if (g + 1 < G) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");  // 13 loads per K block
+    for (int g = 0; g < issued; ++g) {
+      if (g + 1 < issued) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");  // 13 loads per K block
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (g + 2 < G) issue();
+      if (more) issue();
     }
     return;
   }
@@ -852,55 +1028,28 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
   int flo, fhi;
   frag_sw_offsets(lane, flo, fhi);
   int slot = 0;
-  for (int item = first; item < total; item += gridDim.x) {
-    int mg, nt;
-    tiled_item_coords(item, Q1_NT, mg, nt);
-    if (mg >= total_m) continue;
-    const int e = find_expert(map, mg);
-    const int m0 = (mg - map.mt_prefix[e]) * Q1_BM;
+  for (int round = 0;; ++round) {
+    const int i = snake_item(round, my_slot, G);
+    if (i >= total) break;
+    const int it = block_order_item(i, map.total_m, Q1_NT);
+    const int k = it / Q1_NT, nt = it % Q1_NT;
+    int e, m0;
+    tile_row<Q1_BM>(map, k, e, m0);
     const int cnt = map.cnt[e], seg = map.seg[e];
+    // 16-row fragments holding valid rows; this wave's are 2 mt + wm for mt < nmt
+    const int nf = (min(Q1_BM, cnt - m0) + 15) / 16;
+    const int nmt = (nf + 1 - wm) / 2;
     v4f accu[4][2], accg[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
-#pragma unroll 1
-    for (int kb = 0; kb < NB_H; ++kb) {
-      __builtin_amdgcn_s_barrier();  // K block kb is in its slot; the slot before it is free
-      asm volatile("" ::: "memory");
-      const uint8_t* st = q1_lds + slot * W1_STAGE;
-      slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
-      v8i a[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) a[mt] = lds_frag_sw(st + (wm * 4 + mt) * FRAG_BYTES, flo, fhi);
-      v4f pu[4][2], pg[4][2];
-#pragma unroll
-      for (int n2 = 0; n2 < 2; ++n2) {
-        const v8i bu = lds_frag_sw(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
-        const v8i bg = lds_frag_sw(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          pu[mt][n2] = mfma_fp8_k128(a[mt], bu);
-          pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
-        }
-      }
-      const float swu = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF);
-      const float swg = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF + 4);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + (wm * 64 + mt * 16 + 4 * kg) * 4);
-        v4f fu, fg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
-#pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
-            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
-          }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+    switch (nmt) {
+      case 0: g1_loader_kloop<0>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
+      case 1: g1_loader_kloop<1>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
+      case 2: g1_loader_kloop<2>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
+      case 3: g1_loader_kloop<3>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
+      default: g1_loader_kloop<4>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
     }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -908,7 +1057,7 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
       for (int n2 = 0; n2 < 2; ++n2)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * 64 + mt * 16 + 4 * kg + r;
+          const int row = m0 + (2 * mt + wm) * 16 + 4 * kg + r;
           if (row < cnt) {
             const int col = nt * Q1_BNP + wn * 32 + n2 * 16 + fr;
             c_act[(size_t)(seg + row) * I + col] = f32_to_bf16_rne(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
@@ -921,7 +1070,8 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
 // GEMM2 (+ routing weight), prefill shape: 128 rows x 256 output columns per
 // item on the bf16 MFMA v_mfma_f32_32x32x16_bf16 (full bf16 rate; the 16x16x32
 // form runs at well under half of it), 8 compute waves as 2 (rows) x 4
-// (columns), each 64 x 64 = 2 x 2 tiles of 32 x 32, and 4 loader waves.
+// (columns), each 64 x 64 = 2 x 2 tiles of 32 x 32 (row blocks 2 i + wm, so
+// the two row halves interleave), and 4 loader waves.
 //
 // One stage is one 128-wide K block (the W2 scale block): the activation tile
 // (128 rows x 256 B bf16) and the W2 tile (256 rows x 128 B e4m3), 64 KB, in a
@@ -963,24 +1113,107 @@ constexpr int W2_WSCALE_OFF = Q2_STAGE;
 constexpr int W2_STAGE = Q2_STAGE + 16;
 static_assert(W2_LJOBS * W2_PWAVES == 64, "64 load instructions per K block");
 
+// One item for a compute wave of the GEMM2 loader kernel: NI of its 32-row
+// blocks (2 i + wm, i < NI) against its two 32-column W2 blocks over the 16 K
+// blocks, then its rows of the item, times each pair's routing weight, as fp32
+// rows. Row blocks past the item's valid rows are skipped; every wave takes
+// the barrier of every K block whatever its NI. (Each NI runs the whole item,
+// accumulators included, so that no accumulator lives across the choice.)
+struct G2Item {
+  int m0, cnt, seg, nt;
+};
+template <int NI>
+__device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot, int wm, int wn, int lane,
+                                               const G2Item& it, const float* __restrict__ perm_w,
+                                               float* __restrict__ partial) {
+  const int lr = lane & 31, lg = lane >> 5;
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+  int boff[4], aoff[2][2];
+#pragma unroll
+  for (int pp = 0; pp < 4; ++pp) boff[pp] = sw32(lr, 2 * pp + lg);
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) aoff[ph][tt] = sw32(lr, 4 * ph + 2 * lg + tt);
+#pragma unroll 1
+  for (int kb = 0; kb < NB_I; ++kb) {
+    __builtin_amdgcn_s_barrier();  // block kb is in its slot
+    asm volatile("" ::: "memory");
+    const uint8_t* st = q2_lds + slot * W2_STAGE;
+    slot ^= 1;
+    if constexpr (NI > 0) {
+      const uint8_t* sb = st + Q2_A_BYTES + (wn * 2) * Q2_REG;  // this wave's two W2 row blocks
+      v16f pacc[NI][2];
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) pacc[i][j] = v16f{};
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        v8bf bf[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[pp]);
+          bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
+          bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          v8bf af[NI];
+#pragma unroll
+          for (int i = 0; i < NI; ++i)  // row block 2 i + wm: two 128 B halves of the K block
+            af[i] = *reinterpret_cast<const v8bf*>(st + ((2 * i + wm) * 2 + (pp >> 1)) * Q2_REG + aoff[pp & 1][tt]);
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_bf16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
+        }
+      }
+      const float sc = *reinterpret_cast<const float*>(st + W2_WSCALE_OFF + 4 * (wn >> 1));
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += pacc[i][j][r] * sc;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+  }
+  // epilogue: weight by the pair's routing weight, one fp32 row per pair
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
+      if (row < it.cnt) {
+        const float w = perm_w[it.seg + row];
+        float* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
+      }
+    }
+}
+
 __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+    DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   build_tile_map<Q2_BM>(hdr, map);
-  const int total_m = map.mt_prefix[E_LOCAL];
-  const int total = tiled_items(total_m, Q2_NT);
-  const int first = xcd_remap(blockIdx.x, gridDim.x);
-  int n_items = 0;
-  for (int item = first; item < total; item += gridDim.x) {
-    int mg, nt;
-    tiled_item_coords(item, Q2_NT, mg, nt);
-    n_items += mg < total_m;
+  const bool feeder = wave == W2_CWAVES + W2_PWAVES - 1;  // the last loader wave
+  ItemFeed feed;
+  if (feeder && lane == 0) {
+    feed.q.init(hdr->tile_pos, &hdr->tile_done, map.total_m, Q2_NT);
+    feed.ask();
+    map.ring[0] = feed.resolve();
   }
-  const int G = n_items * NB_I;  // K blocks this workgroup runs
+  __syncthreads();
 
   if (wave >= W2_CWAVES) {
     // ----------------------------- loader waves -----------------------------
@@ -990,15 +1223,15 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const bool a_wave = p < 2;
     const uint8_t* src[W2_LJOBS];
     const float* ssrc = s2;
-    int item = first - (int)gridDim.x, kb = NB_I, slot = 0;
-    auto next_item = [&]() {
-      int mg = 0, nt = 0;
-      for (item += gridDim.x; item < total; item += gridDim.x) {
-        tiled_item_coords(item, Q2_NT, mg, nt);
-        if (mg < total_m) break;
-      }
-      const int e = find_expert(map, mg);
-      const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
+    int seq = -1, kb = NB_I, slot = 0, issued = 0;
+    bool more = true;
+    auto next_item = [&]() -> bool {
+      const int it = __builtin_amdgcn_readfirstlane(map.ring[(seq + 1) & 3]);
+      if (it < 0) return false;
+      ++seq;
+      const int k = it / Q2_NT, nt = it % Q2_NT;
+      int e, m0;
+      tile_row<Q2_BM>(map, k, e, m0);
       const int cnt = map.cnt[e], seg = map.seg[e];
 #pragma unroll
       for (int i = 0; i < W2_LJOBS; ++i) {
@@ -1015,9 +1248,14 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
       }
       ssrc = s2 + ((size_t)e * NB_H + 2 * nt + (lane & 1)) * NB_I;
       kb = 0;
+      return true;
     };
     auto issue = [&]() {
-      if (kb == NB_I) next_item();
+      if (kb == NB_I && !(more = next_item())) return;
+      if (feeder && kb == FEED_KB) {
+        if (lane == 0) map.ring[(seq + 1) & 3] = feed.resolve();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the entry is written before this wave's next barrier
+      }
       uint8_t* st = q2_lds + slot * W2_STAGE;
 #pragma unroll
       for (int i = 0; i < W2_LJOBS; ++i) {
@@ -1028,99 +1266,41 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
         lds_direct16(src[i] + (size_t)kb * (a_wave ? 2 * BLK : BLK), st + dst);
       }
       if (p == W2_PWAVES - 1 && lane < 2) lds_direct4(ssrc + kb, st + W2_WSCALE_OFF);
+      if (feeder && kb == 0 && lane == 0) feed.ask();
       slot ^= 1;
       ++kb;
+      ++issued;
     };
-    if (G > 0) issue();
+    issue();
 #pragma unroll 1
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < issued; ++g) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block g
       __builtin_amdgcn_s_barrier();                     // every block-g load landed; block g-1 is read
       asm volatile("" ::: "memory");
-      if (g + 1 < G) issue();
+      if (more) issue();
     }
     return;
   }
 
   // ------------------------------- compute waves -------------------------------
   const int wm = wave & 1, wn = wave >> 1;
-  const int lr = lane & 31, lg = lane >> 5;
-  int boff[4], aoff[2][2];
-#pragma unroll
-  for (int pp = 0; pp < 4; ++pp) boff[pp] = sw32(lr, 2 * pp + lg);
-#pragma unroll
-  for (int ph = 0; ph < 2; ++ph)
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) aoff[ph][tt] = sw32(lr, 4 * ph + 2 * lg + tt);
   int slot = 0;
-  for (int item = first; item < total; item += gridDim.x) {
-    int mg, nt;
-    tiled_item_coords(item, Q2_NT, mg, nt);
-    if (mg >= total_m) continue;
-    const int e = find_expert(map, mg);
-    const int m0 = (mg - map.mt_prefix[e]) * Q2_BM;
+  for (int seq = 0;; ++seq) {
+    const int it = __builtin_amdgcn_readfirstlane(map.ring[seq & 3]);
+    if (it < 0) break;
+    const int k = it / Q2_NT, nt = it % Q2_NT;
+    int e, m0;
+    tile_row<Q2_BM>(map, k, e, m0);
     const int cnt = map.cnt[e], seg = map.seg[e];
-    v16f acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
-#pragma unroll 1
-    for (int kb = 0; kb < NB_I; ++kb) {
-      __builtin_amdgcn_s_barrier();  // block kb is in its slot
-      asm volatile("" ::: "memory");
-      const uint8_t* st = q2_lds + slot * W2_STAGE;
-      slot ^= 1;
-      const uint8_t* sa = st + (wm * 2) * 2 * Q2_REG;           // this wave's two activation row blocks
-      const uint8_t* sb = st + Q2_A_BYTES + (wn * 2) * Q2_REG;  // its two W2 row blocks
-      v16f pacc[2][2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) pacc[i][j] = v16f{};
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        v8bf bf[2][2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[pp]);
-          bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
-          bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
-        }
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          v8bf af[2];
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const v8bf*>(sa + (i * 2 + (pp >> 1)) * Q2_REG + aoff[pp & 1][tt]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_bf16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
-        }
-      }
-      const float sc = *reinterpret_cast<const float*>(st + W2_WSCALE_OFF + 4 * (wn >> 1));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += pacc[i][j][r] * sc;
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+    // 32-row blocks holding valid rows; this wave's are 2 i + wm for i < ni
+    const int nb = (min(Q2_BM, cnt - m0) + 31) / 32;
+    const int ni = (nb + 1 - wm) / 2;
+    const G2Item gi{m0, cnt, seg, nt};
+    switch (ni) {
+      case 0: g2_loader_item<0>(q2_lds, slot, wm, wn, lane, gi, perm_w, partial); break;
+      case 1: g2_loader_item<1>(q2_lds, slot, wm, wn, lane, gi, perm_w, partial); break;
+      default: g2_loader_item<2>(q2_lds, slot, wm, wn, lane, gi, perm_w, partial); break;
     }
-    // epilogue: weight by the pair's routing weight, one fp32 row per pair
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
-        if (row < cnt) {
-          const float w = perm_w[seg + row];
-          float* dst = partial + (size_t)(seg + row) * H + nt * Q2_BN + wn * 64 + lr;
-#pragma unroll
-          for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
-        }
-      }
   }
 }
 
@@ -1205,7 +1385,7 @@ hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const f
 }
 
 hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
-                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
+                               const float* s13, DispatchHeader* hdr, const int32_t* perm_tok,
                                uint16_t* c_act, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
@@ -1219,7 +1399,7 @@ hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
+hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, DispatchHeader* hdr,
                                const float* perm_w, float* partial, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {

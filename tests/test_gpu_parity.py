@@ -314,6 +314,31 @@ def test_graph_replay_matches_eager(case):
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
 
 
+@pytest.mark.parametrize("case", ["prefill_t1024", "skew_t4096"], indirect=True)
+def test_prefill_stages_rerun_alone(case):
+    """The prefill GEMM2 takes its items from work queues whose counters live in
+    the workspace header; its last workgroup resets them. So the GEMM stages
+    launched again on their own (no routing or dispatch in between, as a
+    per-stage replay or a profiler does), GEMM2 twice in a row, recompute the
+    same output, bit for bit, every time."""
+    from flashinfer_mlsys_amd import _lib
+    lib = _lib.load()
+    dev = case.gpu[0].device
+    out = torch.empty((case.w.T, 7168), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(fm.workspace_size(case.w.T), dtype=torch.uint8, device=dev)
+    fm.kernel(*case.gpu, case.offset, case.rsf, out, workspace=ws)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    args = ([t.data_ptr() for t in case.gpu] + [case.w.T, case.offset, case.rsf, out.data_ptr(), ws.data_ptr(),
+                                                 ws.numel(), torch.cuda.current_stream(dev).cuda_stream])
+    for rep in range(3):
+        out.fill_(3.0)
+        for stage in (1, 2, 2, 3):
+            _lib.check(lib.moe_fp8_run_stage(stage, *args), "moe_fp8_run_stage")
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"rerun {rep}"
+
+
 @pytest.mark.parametrize("case", ["t16", "prefill_t1024", "skew_t4096"], indirect=True)
 def test_stale_workspace_is_never_read_as_data(case):
     """The workspace arrives filled with 0xFF bytes (every stale token index reads
