@@ -769,7 +769,7 @@ struct ItemQueue {
   // caller asks no more).
   __device__ int resolve(int q) {
     for (;;) {
-      if (q < len(x)) return item(x, q);
+      if (q >= 0 && q < len(x)) return item(x, q);
       x = (x + 1) % N_XCD;
       if (x == home) break;
       q = atomicAdd(&pos[x], 1);
