@@ -24,10 +24,10 @@ hipError_t launch_router_quantize(const uint16_t*, const uint16_t*, int, float*,
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const int32_t*,
                                const float*, int, uint16_t*, hipStream_t);
 int gemm1_decode_blocks_per_cu();
-hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*, DispatchHeader*,
-                               const int32_t*, uint16_t*, int, hipStream_t);
-hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, DispatchHeader*, const float*, float*,
-                               int, hipStream_t);
+hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*,
+                               const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
+hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
+                               float*, int, hipStream_t);
 hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStream_t);
 }  // namespace moe
 

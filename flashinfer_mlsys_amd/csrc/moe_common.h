@@ -34,20 +34,9 @@ struct DispatchHeader {
   int32_t seg_start[E_LOCAL + 1];  // exclusive scan of counts; seg_start[32] = P
   int32_t n_active;                // experts with count > 0
   int32_t active[E_LOCAL];         // their local ids, ascending
-  // work queues of the prefill GEMM2 kernel (per-XCD positions, and the count
-  // of workgroups done): zero between launches
-  int32_t tile_pos[8];
-  int32_t tile_done;
-  int32_t pad[256 / 4 * 2 - (E_LOCAL * 3 + 2) - 9];
+  int32_t pad[256 / 4 * 2 - (E_LOCAL * 3 + 2)];
 };
 static_assert(sizeof(DispatchHeader) == 512, "header is 512 bytes");
-
-// Plain stores, by the kernel that writes the header; the GEMM kernels of the
-// same stream see them after the kernel boundary.
-__device__ __forceinline__ void clear_tile_queues(DispatchHeader* hdr) {
-  for (int i = 0; i < 8; ++i) hdr->tile_pos[i] = 0;
-  hdr->tile_done = 0;
-}
 
 // One MFMA over a full 128-wide K block: D(16x16 fp32) = A(16x128 e4m3) * B(128x16 e4m3).
 // Lane l holds row (l % 16) of A / column (l % 16) of B and the 32 K values

@@ -630,23 +630,14 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
 // cheapest items, last, where they even out the workgroups' finishing times.
 // The block order: blocks of 8 row tiles x 4 column tiles, row-block major.
 //
-// GEMM1 deals the block order statically in rounds (snake_item): each 32-item
-// block runs on the 32 workgroups of one XCD in step, sharing its 8 activation
-// and 4 weight tiles in that XCD's L2. (Handing its items out at run time, as
-// GEMM2 does, was measured slower: the workgroups of an XCD drift apart and
-// the L2 stops serving the repeats.)
-//
-// GEMM2 hands its items out at run time: the blocks are dealt round robin to 8
-// queues, one per XCD (hardware places workgroup b on XCD b % 8, which only
-// matters for cache locality: correctness never depends on it); the
-// workgroups of an XCD take the items of its queue in order with an atomic
-// position counter, and a workgroup whose queue is empty takes from the next
-// queues in turn. The last workgroup to find every queue empty resets the
-// counters for the next launch (the dispatch kernel zeroes them too, with the
-// rest of the header).
+// Both kernels deal the block order statically in rounds (snake_item): each
+// 32-item block runs on the 32 workgroups of one XCD in step, sharing its 8
+// activation and 4 weight tiles in that XCD's L2. (Handing the items out at run
+// time from per-XCD atomic work queues was measured: slower for GEMM1, whose
+// workgroups then drift apart so that the L2 stops serving the repeats, and no
+// faster for GEMM2.)
 // ---------------------------------------------------------------------------
-constexpr int TB_M = 8, TB_N = 4, N_XCD = 8;
-static_assert(NB_I >= 6 && NB_H >= 6, "the item feed needs K blocks 0 .. 3 and two more");
+constexpr int TB_M = 8, TB_N = 4;
 
 struct TileMap {
   int order[E_LOCAL];     // expert of each rank (descending row count)
@@ -654,7 +645,6 @@ struct TileMap {
   int cnt[E_LOCAL];       // by expert id
   int seg[E_LOCAL];
   int total_m;            // row tiles
-  int ring[4];            // item of sequence number s at ring[s % 4] (-1: no more)
 };
 
 template <int BM>
@@ -699,27 +689,7 @@ __device__ __forceinline__ void tile_row(const TileMap& m, int k, int& e, int& m
   m0 = (k - m.pref[j]) * BM;
 }
 
-// Length of queue x: the blocks b = x + 8 j; only the blocks of the last row
-// block hold fewer than 32 items, and each queue holds at most one of them (its last).
-__device__ __forceinline__ int queue_len(int x, int total_m, int nbk) {
-  const int nrb = (total_m + TB_M - 1) / TB_M, nblocks = nrb * nbk;
-  if (x >= nblocks) return 0;
-  const int nj = (nblocks - x + N_XCD - 1) / N_XCD;
-  const int last = x + N_XCD * (nj - 1);
-  const int rows_last = total_m - TB_M * (nrb - 1);
-  return TB_M * TB_N * nj - (last / nbk == nrb - 1 ? (TB_M - rows_last) * TB_N : 0);
-}
-
-// Position q < queue_len(x) of queue x -> item id k * (4 nbk) + nt.
-__device__ __forceinline__ int queue_item(int x, int q, int total_m, int nbk) {
-  const int nrb = (total_m + TB_M - 1) / TB_M;
-  const int b = x + N_XCD * (q / (TB_M * TB_N)), i = q % (TB_M * TB_N);
-  const int rb = b / nbk, cb = b % nbk;
-  const int rows = rb == nrb - 1 ? total_m - TB_M * rb : TB_M;
-  return (TB_M * rb + i % rows) * (TB_N * nbk) + TB_N * cb + i / rows;
-}
-
-// The static deal (GEMM1): item i of the block order (all blocks row-block
+// The static deal: item i of the block order (all blocks row-block
 // major, the last row block's blocks shorter) -> item id k * nt_count + nt.
 __device__ __forceinline__ int block_order_item(int i, int total_m, int nt_count) {
   const int nbk = nt_count / TB_N, nrb = (total_m + TB_M - 1) / TB_M;
@@ -747,56 +717,6 @@ __device__ __forceinline__ int block_order_item(int i, int total_m, int nt_count
 // one round take the costlier ones of the next.
 __device__ __forceinline__ int snake_item(int r, int slot, int G) { return r * G + ((r & 1) ? G - 1 - slot : slot); }
 
-// The workgroup's item source, used by one lane: pos[8] and done live in the
-// dispatch header.
-struct ItemQueue {
-  int* pos;
-  int* done;
-  int home, x, total_m, nbk;
-
-  __device__ __forceinline__ void init(int* pos_, int* done_, int total_m_, int nt_count) {
-    pos = pos_;
-    done = done_;
-    home = x = blockIdx.x % N_XCD;
-    total_m = total_m_;
-    nbk = nt_count / TB_N;
-  }
-  __device__ __forceinline__ int len(int qx) const { return queue_len(qx, total_m, nbk); }
-  __device__ __forceinline__ int item(int qx, int q) const { return queue_item(qx, q, total_m, nbk); }
-  // The item at position q of queue x if that exists, else the next item from the
-  // following queues in turn; -1 once every queue is empty (and then the
-  // workgroup counts itself out, the last one resetting the counters; the
-  // caller asks no more).
-  __device__ int resolve(int q) {
-    for (;;) {
-      if (q >= 0 && q < len(x)) return item(x, q);
-      x = (x + 1) % N_XCD;
-      if (x == home) break;
-      q = atomicAdd(&pos[x], 1);
-    }
-    if (atomicAdd(done, 1) == (int)gridDim.x - 1) {
-      for (int i = 0; i < N_XCD; ++i) atomicExch(&pos[i], 0);
-      atomicExch(done, 0);
-    }
-    return -1;
-  }
-  __device__ __forceinline__ int ask() { return atomicAdd(&pos[x], 1); }
-};
-
-// Lane 0 of the last loader wave keeps the item ring one item ahead: right
-// after issuing K block 0 of an item it asks for the next position, and before
-// issuing K block FEED_KB it resolves the answer and writes the ring entry
-// (the atomic has had a few K blocks to return; every wave reads the entry at
-// least one barrier later: the loader waves when they start the next item, the
-// compute waves after finishing this one). It lives in a loader wave so that
-// its state takes no registers from the compute waves' MFMA loop.
-constexpr int FEED_KB = 3;
-struct ItemFeed {
-  ItemQueue q;
-  int pending;
-  __device__ __forceinline__ void ask() { pending = q.ask(); }
-  __device__ __forceinline__ int resolve() { return q.resolve(pending); }
-};
 
 // ---------------------------------------------------------------------------
 // GEMM1 + SwiGLU, prefill shape: 128 rows x 128 column pairs (X1 rows n..n+127
@@ -922,14 +842,14 @@ __device__ __forceinline__ void g1_loader_kloop(const uint8_t* q1_lds, int& slot
 
 __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13, DispatchHeader* __restrict__ hdr,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
     const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q1_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   build_tile_map<Q1_BM>(hdr, map);
-  const int total = map.total_m * Q1_NT, G = gridDim.x;
+  const int total = __builtin_amdgcn_readfirstlane(map.total_m) * Q1_NT, G = gridDim.x;
   const int my_slot = xcd_remap(blockIdx.x, G);
 
   if (wave >= W1_CWAVES) {
@@ -942,7 +862,7 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
     const int my_order = lane < E_LOCAL ? map.order[lane] : 0;
     const int my_cnt = lane < E_LOCAL ? map.cnt[lane] : 0;
     const int my_seg = lane < E_LOCAL ? map.seg[lane] : 0;
-    const int map_total_m = map.total_m;
+    const int map_total_m = __builtin_amdgcn_readfirstlane(map.total_m);
     const uint8_t* srcA[W1_AJOBS];
     const uint8_t* srcB[W1_BJOBS];
     const float* ssrc = hscale;
@@ -1200,84 +1120,125 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
 
 __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   build_tile_map<Q2_BM>(hdr, map);
-  const bool feeder = wave == W2_CWAVES + W2_PWAVES - 1;  // the last loader wave
-  ItemFeed feed;
-  if (feeder && lane == 0) {
-    feed.q.init(hdr->tile_pos, &hdr->tile_done, map.total_m, Q2_NT);
-    feed.ask();
-    map.ring[0] = feed.resolve();
-  }
-  __syncthreads();
+  const int total = __builtin_amdgcn_readfirstlane(map.total_m) * Q2_NT, G = gridDim.x;
+  const int my_slot = xcd_remap(blockIdx.x, G);
 
   if (wave >= W2_CWAVES) {
     // ----------------------------- loader waves -----------------------------
-    // Loads complete before every barrier (one block ahead, two slots), so these
-    // waves may read the tile map from LDS: no direct load is in flight then.
+    // Blocks go global -> registers -> LDS. While block g + 1 is in flight into
+    // this wave's other register buffer, block g is written into its LDS slot
+    // (the compute waves finished the block that held the slot before the
+    // previous barrier) and the freed buffer takes block g + 2: two blocks in
+    // flight per CU, where direct global -> LDS loads into the 2-slot ring
+    // allow one. The loads are unconditional buffer loads (a zero-byte range
+    // once no item is left: zeros, no memory access) so that the compiler
+    // counts the loads in flight and waits only for the older block's.
     const int p = wave - W2_CWAVES, ld_row = lane >> 3;
     const bool a_wave = p < 2;
-    const uint8_t* src[W2_LJOBS];
-    const float* ssrc = s2;
-    int seq = -1, kb = NB_I, slot = 0, issued = 0;
+    __amdgpu_buffer_rsrc_t rsrc = buf_rsrc(w2, 0), srsrc = buf_rsrc(s2, 0);
+    const uint32_t step_bytes = a_wave ? 2 * BLK : BLK;  // activation rows advance 256 B per K block, W2 rows 128 B
+    const int map_total_m = __builtin_amdgcn_readfirstlane(map.total_m);
+    const uint32_t row_bytes = a_wave ? I * 2 : I;
+    // Job i (8 rows x 128 B, lane l: row l / 8, 16 B chunk (l % 8) ^ (l / 8) ^
+    // parity) sits at byte job_off(i) + lane_off[i % 2] of the tile: no
+    // per-job registers. Activation jobs: 32-row block 2 p + i / 8, half
+    // (i / 4) % 2 of the 256 B row, 8-row group i % 4; W2 jobs: 32-row block
+    // 4 (p - 2) + i / 4, 8-row group i % 4.
+    uint32_t lane_off[2];
+#pragma unroll
+    for (int par = 0; par < 2; ++par) lane_off[par] = ld_row * row_bytes + (((lane & 7) ^ ld_row ^ par) * 16);
+    auto job_off = [&](int i) -> uint32_t {
+      return a_wave ? (uint32_t)(((2 * p + (i >> 3)) * 32 + (i & 3) * 8) * (I * 2) + ((i >> 2) & 1) * 128)
+                    : (uint32_t)((((p - 2) * 4 + (i >> 2)) * 32 + (i & 3) * 8) * I);
+    };
+    int round = -1, kb = NB_I, nreal = 0;
     bool more = true;
     auto next_item = [&]() -> bool {
-      const int it = __builtin_amdgcn_readfirstlane(map.ring[(seq + 1) & 3]);
-      if (it < 0) return false;
-      ++seq;
+      const int i_next = snake_item(++round, my_slot, G);
+      if (i_next >= total) {
+        rsrc = buf_rsrc(w2, 0);
+        srsrc = buf_rsrc(s2, 0);
+        return false;
+      }
+      const int it = block_order_item(i_next, map_total_m, Q2_NT);
       const int k = it / Q2_NT, nt = it % Q2_NT;
       int e, m0;
       tile_row<Q2_BM>(map, k, e, m0);
-      const int cnt = map.cnt[e], seg = map.seg[e];
-#pragma unroll
-      for (int i = 0; i < W2_LJOBS; ++i) {
-        const int job = p * W2_LJOBS + i, rg = job & 3;
-        const int chunk = (lane & 7) ^ ld_row ^ (rg & 1);
-        if (a_wave) {
-          const int ib = job >> 3, h = (job >> 2) & 1;
-          const int row = seg + min(m0 + ib * 32 + rg * 8 + ld_row, cnt - 1);
-          src[i] = reinterpret_cast<const uint8_t*>(c_act + (size_t)row * I) + h * 128 + chunk * 16;
-        } else {
-          const int jb = (job - 32) >> 2;
-          src[i] = w2 + ((size_t)e * H + nt * Q2_BN + jb * 32 + rg * 8 + ld_row) * I + chunk * 16;
-        }
-      }
-      ssrc = s2 + ((size_t)e * NB_H + 2 * nt + (lane & 1)) * NB_I;
+      e = __builtin_amdgcn_readfirstlane(e);
+      m0 = __builtin_amdgcn_readfirstlane(m0);
+      const int cnt = __builtin_amdgcn_readfirstlane(map.cnt[e]), seg = __builtin_amdgcn_readfirstlane(map.seg[e]);
+      const int valid = min(Q2_BM, cnt - m0);
+      // the activation range ends at the valid rows: rows past it load as zeros
+      // (their output rows are dropped)
+      rsrc = a_wave ? buf_rsrc(c_act + (size_t)(seg + m0) * I, (uint32_t)valid * I * 2)
+                    : buf_rsrc(w2 + ((size_t)e * H + nt * Q2_BN) * I, (uint32_t)Q2_BN * I);
+      // the block scales of output column blocks 2 nt and 2 nt + 1
+      srsrc = buf_rsrc(s2 + ((size_t)e * NB_H + 2 * nt) * NB_I, 2 * NB_I * 4);
       kb = 0;
       return true;
     };
-    auto issue = [&]() {
-      if (kb == NB_I && !(more = next_item())) return;
-      if (feeder && kb == FEED_KB) {
-        if (lane == 0) map.ring[(seq + 1) & 3] = feed.resolve();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the entry is written before this wave's next barrier
+    auto load_block = [&](v4i (&buf)[W2_LJOBS], float& sv) {
+      if (kb == NB_I && more) more = next_item();
+      const int kk = more ? kb : 0;
+      // the scale first: a later load into the same register then waits for this
+      // small load alone, not for the block's data loads behind it
+      // (the order of the loads is pinned: the same in every copy of this code,
+      // so that the compiler's count of the loads in flight agrees at the loop head)
+      __builtin_amdgcn_sched_barrier(0);
+      sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, (uint32_t)(((lane & 1) * NB_I + kk) * 4), 0, 0));
+#pragma unroll
+      for (int i = 0; i < W2_LJOBS; ++i) {
+        __builtin_amdgcn_sched_barrier(0);
+        buf[i] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off[i & 1] + job_off(i), kk * step_bytes, 0));
       }
-      uint8_t* st = q2_lds + slot * W2_STAGE;
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) {
+        ++kb;
+        ++nreal;
+      }
+    };
+    auto store_block = [&](int g, const v4i (&buf)[W2_LJOBS], float sv) {
+      uint8_t* st = q2_lds + (g & 1) * W2_STAGE;
 #pragma unroll
       for (int i = 0; i < W2_LJOBS; ++i) {
         const int job = p * W2_LJOBS + i, rg = job & 3;
         const int dst = a_wave ? ((job >> 3) * 2 + ((job >> 2) & 1)) * Q2_REG + rg * 1024
                                : Q2_A_BYTES + ((job - 32) >> 2) * Q2_REG + rg * 1024;
-        // activation rows advance 256 B per K block, W2 rows 128 B
-        lds_direct16(src[i] + (size_t)kb * (a_wave ? 2 * BLK : BLK), st + dst);
+        *reinterpret_cast<v4i*>(st + dst + 16 * lane) = buf[i];
       }
-      if (p == W2_PWAVES - 1 && lane < 2) lds_direct4(ssrc + kb, st + W2_WSCALE_OFF);
-      if (feeder && kb == 0 && lane == 0) feed.ask();
-      slot ^= 1;
-      ++kb;
-      ++issued;
+      if (p == W2_PWAVES - 1 && lane < 2) *reinterpret_cast<float*>(st + W2_WSCALE_OFF + 4 * lane) = sv;
     };
-    issue();
+    v4i buf0[W2_LJOBS], buf1[W2_LJOBS];
+    float sv0, sv1;
+    load_block(buf0, sv0);
+    load_block(buf1, sv1);
+    // Two blocks per pass, every load and store unconditional (one path through
+    // the loop for the compiler's count of loads in flight). When block g + 1
+    // does not exist its store writes zeros into a slot no wave reads any more
+    // (block g - 1's, finished before barrier g), and its barrier is skipped.
+    int g = 0;
+    if (nreal > 0) {
 #pragma unroll 1
-    for (int g = 0; g < issued; ++g) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block g
-      __builtin_amdgcn_s_barrier();                     // every block-g load landed; block g-1 is read
-      asm volatile("" ::: "memory");
-      if (more) issue();
+      do {
+        store_block(g, buf0, sv0);  // block g; its slot held block g - 2, read before the last barrier
+        load_block(buf0, sv0);      // block g + 2
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // block g is in its slot; block g - 1 is read
+        asm volatile("" ::: "memory");
+        store_block(g + 1, buf1, sv1);
+        load_block(buf1, sv1);  // block g + 3
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (g + 1 < nreal) __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        g += 2;
+      } while (g < nreal);
     }
     return;
   }
@@ -1285,9 +1246,10 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
   // ------------------------------- compute waves -------------------------------
   const int wm = wave & 1, wn = wave >> 1;
   int slot = 0;
-  for (int seq = 0;; ++seq) {
-    const int it = __builtin_amdgcn_readfirstlane(map.ring[seq & 3]);
-    if (it < 0) break;
+  for (int round = 0;; ++round) {
+    const int i = snake_item(round, my_slot, G);
+    if (i >= total) break;
+    const int it = block_order_item(i, map.total_m, Q2_NT);
     const int k = it / Q2_NT, nt = it % Q2_NT;
     int e, m0;
     tile_row<Q2_BM>(map, k, e, m0);
@@ -1385,7 +1347,7 @@ hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const f
 }
 
 hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
-                               const float* s13, DispatchHeader* hdr, const int32_t* perm_tok,
+                               const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
                                uint16_t* c_act, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
@@ -1399,7 +1361,7 @@ hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, DispatchHeader* hdr,
+hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
                                const float* perm_w, float* partial, int grid, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {

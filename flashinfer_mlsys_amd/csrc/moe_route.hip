@@ -71,7 +71,6 @@ __global__ __launch_bounds__(256) void dispatch_kernel(const int32_t* __restrict
       hdr->seg_start[E_LOCAL] = acc;
       hdr->n_active = nact;
       for (int e = nact; e < E_LOCAL; ++e) hdr->active[e] = -1;
-      clear_tile_queues(hdr);
     }
   }
   __syncthreads();
@@ -198,7 +197,6 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
       hdr->seg_start[E_LOCAL] = acc;
       hdr->n_active = nact;
       for (int e = nact; e < E_LOCAL; ++e) hdr->active[e] = -1;
-      clear_tile_queues(hdr);
     }
   }
   // this chunk's tokens: which local experts each selected, and in which slot

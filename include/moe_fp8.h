@@ -99,9 +99,7 @@ int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int
  * cumsum dispatch of solution/cuda/kernel_v2.cu:208-244, without its host sync).
  * From the routing stage's ids and weights, writes
  *   header   int32 [128]: counts[32], seg_start[33] (seg_start[32] = P),
- *            n_active, active[32] (local ids with tokens, ascending), then
- *            9 words of work-queue state for the operator's own GEMM kernels
- *            (written as zeros), padding
+ *            n_active, active[32] (local ids with tokens, ascending), padding
  *   perm_tok int32 [8T]: for each local expert in order, its tokens ascending
  *   perm_w   fp32  [8T]: the routing weight of each (token, expert) pair
  *   tok_pair int32 [T, 8]: pair index of slot j of token t; must hold -1 on

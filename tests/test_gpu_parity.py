@@ -316,11 +316,10 @@ def test_graph_replay_matches_eager(case):
 
 @pytest.mark.parametrize("case", ["prefill_t1024", "skew_t4096"], indirect=True)
 def test_prefill_stages_rerun_alone(case):
-    """The prefill GEMM2 takes its items from work queues whose counters live in
-    the workspace header; its last workgroup resets them. So the GEMM stages
-    launched again on their own (no routing or dispatch in between, as a
-    per-stage replay or a profiler does), GEMM2 twice in a row, recompute the
-    same output, bit for bit, every time."""
+    """The GEMM stages launched again on their own (no routing or dispatch in
+    between, as a per-stage replay or a profiler does), GEMM2 twice in a row,
+    recompute the same output, bit for bit, every time: the kernels keep no
+    state in the workspace between launches beyond the dispatch they read."""
     from flashinfer_mlsys_amd import _lib
     lib = _lib.load()
     dev = case.gpu[0].device
