@@ -188,7 +188,22 @@ def cpu_baseline(sweep_names):
                   "ref_moe.py that dequantises all 32 experts to fp32 per call like the reference",
         "seconds": round(tot_t, 2),
         "us_per_call_mean": round(tot_t / len(sweep_names) * 1e6, 1),
+        "host_cpus": os.cpu_count(),
+        "cpu_model": _cpu_model(),
+        "torch": torch.__version__,
     }
+
+
+def _cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 COPY_BYTES = 1 << 30  # calibration kernel: reads and writes 1 GiB (4x the MALL)

@@ -445,11 +445,15 @@ struct G2Shared {
   int nact;
   float pw[SMALL_P];    // pair -> routing weight
   int ptok[SMALL_P];    // pair -> token
-  float red[2][D2_WAVES][2][4][64];
-  float acc[SMALL_T][32];  // token x column accumulators
+  float red[2][D2_WAVES][2][4][64];  // lane index rotated by red_rot (bank-conflict-free reads)
+  float acc[SMALL_T][33];  // token x column accumulators (row stride 33: the rows of two tokens never share banks)
 };
 
-// Weights of expert le for this workgroup's columns c0 .. c0 + 27, this wave's 2 K blocks.
+// The cross-wave sum reads, per wave, 4 (column block, row) rows of red at the
+// same 16 lane indices; rotating each row's lane index by 16 (2 cb + r) puts
+// those 4 rows on 4 different groups of 16 banks.
+__device__ __forceinline__ int red_rot(int cb, int r, int lane) { return (lane + 16 * ((2 * cb + r) & 3)) & 63; }
+
 // Weights of expert le for this workgroup's columns c0 .. c0 + 27, this wave's 2 K blocks.
 __device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __restrict__ w2, int le, int c0, int kb0) {
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
@@ -531,7 +535,7 @@ __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][cb][r][lane] = acc[cb][r];
+      for (int r = 0; r < 4; ++r) red[wave][cb][r][red_rot(cb, r, lane)] = acc[cb][r];
     lds_barrier();
     {
       // thread (row, col): pair row m0 + row, column col; MFMA lane (kg, fr) holds
@@ -540,7 +544,7 @@ __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b
       if (col < D2_COLS && m0 + row < cnt) {
         float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < D2_WAVES; ++w) v += red[w][cb][r][src];
+        for (int w = 0; w < D2_WAVES; ++w) v += red[w][cb][r][red_rot(cb, r, src)];
         const int pr = seg + m0 + row;
         sh.acc[sh.ptok[pr]][col] += __fmul_rn(v, sh.pw[pr]);  // product rounded, then the sum
       }
@@ -565,7 +569,7 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     sh.seg[E_LOCAL] = hdr->seg_start[E_LOCAL];
     sh.nact = hdr->n_active;
   }
-  for (int i = tid; i < SMALL_T * 32; i += 64 * D2_WAVES) (&sh.acc[0][0])[i] = 0.f;
+  for (int i = tid; i < SMALL_T * 33; i += 64 * D2_WAVES) (&sh.acc[0][0])[i] = 0.f;
   __syncthreads();
   const int nact = __builtin_amdgcn_readfirstlane(sh.nact);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kb0 = wave * D2_KPW;
