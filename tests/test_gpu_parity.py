@@ -240,6 +240,20 @@ def test_no_local_expert_gives_zeros(case, offset):
     assert (out.view(torch.int16) == 0).all()
 
 
+@pytest.mark.parametrize("case", ["t16", "prefill_t1024"], indirect=True)
+@pytest.mark.parametrize("offset", [256, -1000])
+def test_no_local_expert_gives_zeros_prefill_kernels(case, offset):
+    """No pair for the local experts through the prefill kernels (zero row tiles:
+    every GEMM workgroup has no item), whatever T: exact zeros."""
+    old = fm.set_path(2)
+    try:
+        out = case.forward(offset)
+        torch.cuda.synchronize()
+    finally:
+        fm.set_path(old)
+    assert (out.view(torch.int16) == 0).all()
+
+
 @pytest.mark.parametrize("case", ["t16"], indirect=True)
 @pytest.mark.parametrize("offset", [224, 240, -16, 32])
 def test_other_offsets_match_oracle(case, offset):
