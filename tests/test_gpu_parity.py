@@ -282,6 +282,51 @@ ODD_CASES = [(3, 0, 7003, 2.5), (9, 96, 7009, 2.5), (65, 224, 7065, 2.5), (100, 
              (257, 0, 7257, 2.5), (513, 160, 7513, 2.5)]
 
 
+# Rows per local expert at the prefill kernels' edges: 16-row fragments (GEMM1),
+# 32-row blocks (GEMM2), 128-row tiles, and an empty expert among full ones.
+EDGE_COUNTS = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 95, 96, 97, 127, 128, 129, 0, 255, 256, 257]
+
+
+def _routing_for_counts(counts, offset, seed):
+    """Logits that send exactly counts[e] tokens to local expert offset + e: each
+    token's top-8 is its one local expert plus 3 + 2 + 2 experts of three other
+    groups (every chosen logit in [6, 7), every other -8), in shuffled token order."""
+    rng = np.random.default_rng(seed)
+    assign = np.repeat(np.arange(len(counts)), counts)
+    rng.shuffle(assign)
+    T = len(assign)
+    logits = np.full((T, 256), -8.0, dtype=np.float32)
+    others = [g for g in range(8) if g != offset // 32]
+    for t in range(T):
+        logits[t, offset + assign[t]] = 6.0 + rng.random()
+        for g, n in zip(rng.choice(others, 3, replace=False), (3, 2, 2)):
+            logits[t, g * 32 + rng.choice(32, n, replace=False)] = 6.0 + rng.random(n)
+    return torch.from_numpy(logits), torch.zeros(256, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("offset", [0, 96])
+def test_expert_row_counts_at_tile_edges_match_oracle(weights, dev, offset):
+    """Experts with 1, 15, 16, 17, ..., 127, 128, 129, 255, 256, 257 rows: the
+    prefill GEMMs skip row groups past each tile's valid rows, so every fragment,
+    block and tile boundary is exercised; the dispatch counts are exactly those,
+    and the output is within the bar of the CPU oracle."""
+    lg, b = _routing_for_counts(EDGE_COUNTS, offset, 4242 + offset)
+    T = lg.shape[0]
+    _say(f"edge counts T={T} offset={offset}")
+    g, e = cpu_ref.selection_margins(lg, b)
+    assert min(g, e) >= 8
+    hs, hss = wl.quantize_1x128(wl.hidden_bf16(T, 4343 + offset).to(torch.float32))
+    gpu = [t.to(dev) for t in (lg, b, hs, hss)] + list(weights[1])
+    ids, w, pair = fm.route(gpu[0], gpu[1], 2.5)
+    header = fm.dispatch(ids, w, pair, offset)[0].cpu().numpy()
+    want = np.zeros(32, dtype=np.int64)
+    want[:len(EDGE_COUNTS)] = EDGE_COUNTS
+    np.testing.assert_array_equal(header[:32], want)
+    out = fm.run(*gpu, offset, 2.5).float().cpu().numpy()
+    ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, 2.5).float().numpy()
+    assert_close_bf16(out, ref, f"edge counts offset={offset}")
+
+
 @pytest.mark.parametrize("T,offset,seed,rsf", ODD_CASES)
 def test_odd_token_counts_match_oracle(weights, dev, T, offset, seed, rsf):
     """Selection bit-exact and the whole output within the bar of the CPU oracle."""
