@@ -327,6 +327,31 @@ def test_expert_row_counts_at_tile_edges_match_oracle(weights, dev, offset):
     assert_close_bf16(out, ref, f"edge counts offset={offset}")
 
 
+DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48]]
+
+
+@pytest.mark.parametrize("counts", DECODE_EDGE_COUNTS, ids=["64", "33-31", "17-16-15-1-0-15", "1x32", "last48"])
+@pytest.mark.parametrize("path", [0, 2], ids=["auto", "prefill"])
+def test_decode_row_counts_at_pass_edges_match_oracle(weights, dev, counts, path):
+    """At most 64 tokens with the local rows packed on few experts (a 64-row
+    expert, 16 / 17 / 31 / 33 rows, every expert with one row, only the last
+    expert): the decode kernels' 16-row passes and the prefill kernels (forced)
+    both match the CPU oracle."""
+    offset = 32
+    lg, b = _routing_for_counts(counts, offset, 5151 + len(counts))
+    T = lg.shape[0]
+    _say(f"decode edge counts T={T} {counts} path={path}")
+    hs, hss = wl.quantize_1x128(wl.hidden_bf16(T, 5252 + T).to(torch.float32))
+    gpu = [t.to(dev) for t in (lg, b, hs, hss)] + list(weights[1])
+    old = fm.set_path(path)
+    try:
+        out = fm.run(*gpu, offset, 2.5).float().cpu().numpy()
+    finally:
+        fm.set_path(old)
+    ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, 2.5).float().numpy()
+    assert_close_bf16(out, ref, f"counts={counts} path={path}")
+
+
 @pytest.mark.parametrize("T,offset,seed,rsf", ODD_CASES)
 def test_odd_token_counts_match_oracle(weights, dev, T, offset, seed, rsf):
     """Selection bit-exact and the whole output within the bar of the CPU oracle."""
