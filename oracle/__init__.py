@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product path imports this package:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may use it, and only as the checker (or the timed CPU baseline),
+``bench.py`` may use it, and only to check results (or as the timed CPU baseline),
 never as the computation that is shipped or measured on the GPU.
 
 * ``cpu_ref``  -- a PyTorch-on-CPU restatement of ``reference moe/ref_moe.py:4-168``
