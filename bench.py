@@ -91,7 +91,7 @@ class Runner:
         _lib.check(self.lib.moe_fp8_forward(*self._args(c)), "moe_fp8_forward")
 
     def stage(self, c: Case, s: int):
-        _lib.check(self.lib.moe_fp8_run_stage(s, *self._args(c)), "moe_fp8_run_stage")
+        _lib.check(self.lib.moe_fp8_run_stage(s, _lib.MOE_SHAPE_AUTO, *self._args(c)), "moe_fp8_run_stage")
 
     def graph(self, fn, reps):
         """A HIP graph holding `reps` back-to-back calls of fn (captured on torch's stream)."""

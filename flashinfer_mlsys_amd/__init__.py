@@ -26,7 +26,13 @@ import torch
 from . import _lib
 
 __all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_activations", "router_logits",
-           "router_logits_and_quantize", "workspace_size", "MoEInputError", "set_path"]
+           "router_logits_and_quantize", "workspace_size", "MoEInputError", "run_shape", "SHAPE_AUTO",
+           "SHAPE_PREFILL"]
+
+# Expert-GEMM kernel shapes for run_shape / route_dispatch (include/moe_fp8.h MOE_SHAPE_*):
+# the decode kernels up to 64 tokens and the prefill kernels above, or the prefill kernels always.
+SHAPE_AUTO = 0
+SHAPE_PREFILL = 1
 
 H = 7168
 I = 2048
@@ -64,14 +70,6 @@ def workspace_size(T: int) -> int:
     return int(_lib.load().moe_fp8_workspace_size(int(T)))
 
 
-def set_path(path: int) -> int:
-    """Expert-GEMM shape: 0 by token count, 1 decode shape, 2 prefill shape. Returns the old value."""
-    r = _lib.load().moe_fp8_set_path(int(path))
-    if r < 0:
-        raise ValueError("path must be 0, 1 or 2")
-    return r
-
-
 def _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale):
     names = ["routing_logits", "routing_bias", "hidden_states", "hidden_states_scale", "gemm1_weights",
@@ -105,11 +103,9 @@ def _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, 
     return T
 
 
-@torch.no_grad()
-def kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
-           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-           routed_scaling_factor, output, workspace=None):
-    """Destination-passing operator: writes bf16 [T, 7168] into ``output``; returns None."""
+def _forward(shape, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+             routed_scaling_factor, output, workspace):
     T = _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
     _on_gpu(output, "output")
@@ -127,13 +123,26 @@ def kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gem
     out = output if (output.is_contiguous() and output.data_ptr() % 16 == 0) else torch.empty_like(
         output, memory_format=torch.contiguous_format)
     with torch.cuda.device(hidden_states.device):
-        code = lib.moe_fp8_forward(*[a.data_ptr() for a in args], T, int(local_expert_offset),
-                                   float(routed_scaling_factor), out.data_ptr(), workspace.data_ptr(),
-                                   workspace.numel() * workspace.element_size(), _stream(hidden_states.device))
+        tail = (T, int(local_expert_offset), float(routed_scaling_factor), out.data_ptr(), workspace.data_ptr(),
+                workspace.numel() * workspace.element_size(), _stream(hidden_states.device))
+        if shape == SHAPE_AUTO:
+            code = lib.moe_fp8_forward(*[a.data_ptr() for a in args], *tail)
+        else:
+            code = lib.moe_fp8_forward_shape(int(shape), *[a.data_ptr() for a in args], *tail)
     _lib.check(code, "moe_fp8_forward")
     if out is not output:
         output.copy_(out)
     return None
+
+
+@torch.no_grad()
+def kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+           routed_scaling_factor, output, workspace=None):
+    """Destination-passing operator: writes bf16 [T, 7168] into ``output``; returns None."""
+    _forward(SHAPE_AUTO, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor,
+             output, workspace)
 
 
 @torch.no_grad()
@@ -145,6 +154,21 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     output = torch.empty((T, H), dtype=torch.bfloat16, device=hidden_states.device)
     kernel(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
            gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, output)
+    return output
+
+
+@torch.no_grad()
+def run_shape(shape, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor):
+    """``run`` with the expert-GEMM kernel shape chosen for this call (SHAPE_AUTO or
+    SHAPE_PREFILL): tests run both shapes on the same inputs."""
+    _req(shape in (SHAPE_AUTO, SHAPE_PREFILL), "shape must be SHAPE_AUTO or SHAPE_PREFILL")
+    _on_gpu(hidden_states, "hidden_states")
+    T = routing_logits.shape[0]
+    output = torch.empty((T, H), dtype=torch.bfloat16, device=hidden_states.device)
+    _forward(shape, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+             gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor,
+             output, None)
     return output
 
 
@@ -297,8 +321,8 @@ def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
 
 
 @torch.no_grad()
-def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor):
-    """Routing + dispatch exactly as ``kernel`` runs them.
+def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor, shape=SHAPE_AUTO):
+    """Routing + dispatch exactly as ``run_shape(shape, ...)`` runs them.
 
     Returns (topk_ids int32 [T, 8], topk_w fp32 [T, 8], header int32 [128],
     perm_tok int32 [8T], perm_w fp32 [8T], tok_pair int32 [T, 8]).
@@ -319,7 +343,7 @@ def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_sca
         return ids, w, header, perm_tok, perm_w, pair
     lg, b = _contig(routing_logits), _contig(routing_bias.reshape(-1))
     with torch.cuda.device(dev):
-        code = _lib.load().moe_fp8_route_dispatch(lg.data_ptr(), b.data_ptr(), T, int(local_expert_offset),
+        code = _lib.load().moe_fp8_route_dispatch(int(shape), lg.data_ptr(), b.data_ptr(), T, int(local_expert_offset),
                                                   float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(),
                                                   header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
                                                   pair.data_ptr(), _stream(dev))

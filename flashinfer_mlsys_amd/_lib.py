@@ -17,6 +17,10 @@ MOE_ERR_SIZE = -2
 MOE_ERR_ALIGN = -3
 MOE_ERR_WORKSPACE = -4
 MOE_ERR_HIP = -5
+MOE_ERR_ARG = -6
+
+MOE_SHAPE_AUTO = 0
+MOE_SHAPE_PREFILL = 1
 
 # Every symbol the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -25,15 +29,17 @@ SIGNATURES = {
     "moe_fp8_workspace_size": (ctypes.c_size_t, [_I64]),
     "moe_fp8_forward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double, _P, _P,
                                        ctypes.c_size_t, _P]),
-    "moe_fp8_run_stage": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double,
-                                         _P, _P, ctypes.c_size_t, _P]),
+    "moe_fp8_forward_shape": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                             ctypes.c_double, _P, _P, ctypes.c_size_t, _P]),
+    "moe_fp8_run_stage": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                         ctypes.c_double, _P, _P, ctypes.c_size_t, _P]),
     "moe_fp8_route": (ctypes.c_int, [_P, _P, _I64, ctypes.c_double, _P, _P, _P, _P]),
     "moe_fp8_quantize_activations": (ctypes.c_int, [_P, _I64, _P, _P, _P]),
     "moe_fp8_router_logits": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "moe_fp8_router_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
     "moe_fp8_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "moe_fp8_route_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P, _P, _P, _P, _P]),
-    "moe_fp8_set_path": (ctypes.c_int, [ctypes.c_int]),
+    "moe_fp8_route_dispatch": (ctypes.c_int, [ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P, _P, _P,
+                                              _P, _P]),
     "moe_fp8_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "moe_fp8_last_hip_error": (ctypes.c_char_p, []),
     "moe_fp8_abi_version": (ctypes.c_int, []),

@@ -37,7 +37,6 @@ constexpr int kMaxDevices = 64;
 constexpr int kDecodeMaxTokens = 64;        // decode shape (LDS dispatch, streaming GEMMs) up to this many tokens
 constexpr int kRouteInGemm1MaxTokens = 8;   // and routing inside GEMM1 (one token per wave) up to this many
 std::atomic<int> g_cu_count[kMaxDevices];
-std::atomic<int> g_path{0};
 thread_local const char* t_last_hip_error = "no error";
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -86,7 +85,7 @@ struct Call {
   int offset;
   float rsf;
   uint16_t* out;
-  bool decode;  // T <= 64 and not forced to the prefill shape
+  bool decode;  // T <= 64 and the shape is not forced to the prefill kernels
   hipStream_t stream;
   moe::DispatchHeader* hdr;
   int32_t *topk_ids, *tok_pair, *perm_tok;
@@ -98,8 +97,9 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
                const float* hidden_states_scale, const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
                const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
                double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes, void* stream,
-               Call& c) {
+               int shape, Call& c) {
   using namespace moe;
+  if (shape != MOE_SHAPE_AUTO && shape != MOE_SHAPE_PREFILL) return MOE_ERR_ARG;
   if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!routing_logits || !routing_bias || !hidden_states || !hidden_states_scale || !gemm1_weights ||
@@ -124,7 +124,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   c.offset = clamp_offset(local_expert_offset);
   c.rsf = (float)routed_scaling_factor;
   c.out = output;
-  c.decode = g_path.load(std::memory_order_relaxed) != 2 && T <= kDecodeMaxTokens;
+  c.decode = shape == MOE_SHAPE_AUTO && T <= kDecodeMaxTokens;
   c.stream = reinterpret_cast<hipStream_t>(stream);
   c.hdr = reinterpret_cast<DispatchHeader*>(ws + L.hdr);
   c.topk_ids = reinterpret_cast<int32_t*>(ws + L.topk_ids);
@@ -181,16 +181,15 @@ hipError_t run_stage(int stage, const Call& c) {
 
 extern "C" {
 
-int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
-                    const float* hidden_states_scale, const uint8_t* gemm1_weights,
-                    const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
-                    const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
-                    double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+static int forward(int shape, const float* routing_logits, const uint16_t* routing_bias,
+                   const uint8_t* hidden_states, const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                   const float* gemm1_weights_scale, const uint8_t* gemm2_weights, const float* gemm2_weights_scale,
+                   int64_t T, int64_t local_expert_offset, double routed_scaling_factor, uint16_t* output,
+                   void* workspace, size_t workspace_bytes, void* stream) {
   Call c;
   const int v = check_call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
-                           routed_scaling_factor, output, workspace, workspace_bytes, stream, c);
+                           routed_scaling_factor, output, workspace, workspace_bytes, stream, shape, c);
   if (v <= 0) return v;
   for (int stage = 0; stage < 4; ++stage) {
     const hipError_t e = run_stage(stage, c);
@@ -199,17 +198,39 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
   return MOE_OK;
 }
 
-int moe_fp8_run_stage(int stage, const float* routing_logits, const uint16_t* routing_bias,
+int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                    const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                    const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                    const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                    double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return forward(MOE_SHAPE_AUTO, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                 gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                 routed_scaling_factor, output, workspace, workspace_bytes, stream);
+}
+
+int moe_fp8_forward_shape(int shape, const float* routing_logits, const uint16_t* routing_bias,
+                          const uint8_t* hidden_states, const float* hidden_states_scale,
+                          const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
+                          const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T,
+                          int64_t local_expert_offset, double routed_scaling_factor, uint16_t* output,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return forward(shape, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                 gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                 routed_scaling_factor, output, workspace, workspace_bytes, stream);
+}
+
+int moe_fp8_run_stage(int stage, int shape, const float* routing_logits, const uint16_t* routing_bias,
                       const uint8_t* hidden_states, const float* hidden_states_scale, const uint8_t* gemm1_weights,
                       const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
                       const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
                       double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
                       void* stream) {
-  if (stage < 0 || stage > 3) return MOE_ERR_SIZE;
+  if (stage < 0 || stage > 3) return MOE_ERR_ARG;
   Call c;
   const int v = check_call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
-                           routed_scaling_factor, output, workspace, workspace_bytes, stream, c);
+                           routed_scaling_factor, output, workspace, workspace_bytes, stream, shape, c);
   if (v <= 0) return v;
   const hipError_t e = run_stage(stage, c);
   return e == hipSuccess ? MOE_OK : hip_fail(e);
@@ -242,11 +263,12 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
-int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
+int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                            int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
                            float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
                            void* stream) {
   using namespace moe;
+  if (shape != MOE_SHAPE_AUTO && shape != MOE_SHAPE_PREFILL) return MOE_ERR_ARG;
   if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!routing_logits || !routing_bias || !topk_ids || !topk_w || !header || !perm_tok || !perm_w || !tok_pair)
@@ -259,7 +281,7 @@ int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   auto* hdr = reinterpret_cast<DispatchHeader*>(header);
   hipError_t e;
-  const bool decode = g_path.load(std::memory_order_relaxed) != 2 && t <= kDecodeMaxTokens;
+  const bool decode = shape == MOE_SHAPE_AUTO && t <= kDecodeMaxTokens;
   e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, decode ? nullptr : tok_pair, s);
   if (e == hipSuccess) {
     e = decode ? launch_dispatch_small(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)
@@ -303,11 +325,6 @@ int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_we
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
-int moe_fp8_set_path(int path) {
-  if (path < 0 || path > 2) return -1;
-  return g_path.exchange(path);
-}
-
 const char* moe_fp8_strerror(int code) {
   switch (code) {
     case MOE_OK: return "ok";
@@ -316,12 +333,13 @@ const char* moe_fp8_strerror(int code) {
     case MOE_ERR_ALIGN: return "a pointer is not 16-byte aligned";
     case MOE_ERR_WORKSPACE: return "workspace smaller than moe_fp8_workspace_size(T)";
     case MOE_ERR_HIP: return "HIP launch failed";
+    case MOE_ERR_ARG: return "an enumerated argument (stage, shape) is out of range";
     default: return "unknown error";
   }
 }
 
 const char* moe_fp8_last_hip_error(void) { return t_last_hip_error; }
 
-int moe_fp8_abi_version(void) { return 1; }
+int moe_fp8_abi_version(void) { return 2; }
 
 }  // extern "C"

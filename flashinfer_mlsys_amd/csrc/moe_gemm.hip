@@ -30,6 +30,7 @@
 //                consecutive items, which share the weight tile, so that XCD's
 //                L2 serves the repeats.
 #include "moe_common.h"
+#include "moe_host.h"
 #include "moe_route_token.h"
 #include "moe_small_dispatch.h"
 #include "moe_tile.h"
@@ -350,7 +351,9 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const int lane = threadIdx.x & 63;
   if (route_here) {
     const int w = threadIdx.x >> 6;
-    if (w < T) route_token(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr);
+    // tie scratch: the wave's activation stage, first written after the barrier below
+    if (w < T)
+      route_token(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr, reinterpret_cast<TieScratch*>(&sh.a[w][0][0][0]));
     lds_barrier();
     if (blockIdx.x == 0 && (int)threadIdx.x < T * TOP_K) {
       topk_ids[threadIdx.x] = sh.d.ids[threadIdx.x];
@@ -1306,24 +1309,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 namespace moe {
 
 static hipError_t gemm1_decode_set_lds() {
-  static bool done = false;
-  if (done) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_decode_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(G1Shared));
-  if (e == hipSuccess) done = true;
+  static PerDeviceOnce<hipError_t> once;
+  hipError_t e = hipErrorInvalidDevice;
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_decode_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(G1Shared)); },
+           e);
   return e;
 }
 
 int gemm1_decode_blocks_per_cu() {
-  static int cached = 0;
-  if (cached > 0) return cached;
-  int n = 0;
-  if (gemm1_decode_set_lds() != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm1_decode_kernel, 64 * D1_WAVES, sizeof(G1Shared)) !=
-          hipSuccess ||
-      n < 1)
-    n = 1;
-  cached = n;
+  static PerDeviceOnce<int> once;
+  int n = 1;
+  once.get([] {
+    int k = 0;
+    if (gemm1_decode_set_lds() != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemm1_decode_kernel, 64 * D1_WAVES, sizeof(G1Shared)) !=
+            hipSuccess ||
+        k < 1)
+      k = 1;
+    return k;
+  }, n);
   return n;
 }
 
@@ -1353,13 +1358,12 @@ hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const f
 hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
                                const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
                                uint16_t* c_act, int grid, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_loader_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * W1_STAGE);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static PerDeviceOnce<hipError_t> once;
+  hipError_t e = hipErrorInvalidDevice;
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_loader_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * W1_STAGE); },
+           e);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gemm1_loader_kernel, dim3(grid), dim3(W1_THREADS), Q1_NSTAGE * W1_STAGE, stream, hidden,
                      hscale, T, w13, s13, hdr, perm_tok, c_act);
   return hipGetLastError();
@@ -1367,13 +1371,12 @@ hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T
 
 hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
                                const float* perm_w, float* partial, int grid, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_loader_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 2 * W2_STAGE);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static PerDeviceOnce<hipError_t> once;
+  hipError_t e = hipErrorInvalidDevice;
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_loader_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 2 * W2_STAGE); },
+           e);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gemm2_loader_kernel, dim3(grid), dim3(W2_THREADS), 2 * W2_STAGE, stream, c_act, w2, s2, hdr,
                      perm_w, partial);
   return hipGetLastError();

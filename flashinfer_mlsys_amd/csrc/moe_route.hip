@@ -4,8 +4,9 @@
 //                     group scores, top-4 of 8 groups, top-8 experts inside them,
 //                     weights from the unbiased sigmoid normalised over the 8 and
 //                     scaled). One wave64 per token, 4 experts per lane; the
-//                     top-8 is a ballot/popcount threshold search (no serial
-//                     arg-max rounds).
+//                     top-8 by 8 rounds of wave arg-max, and the reference's
+//                     nth_element order where equal keys straddle a cut
+//                     (moe_route_token.h, moe_route_ties.h).
 // dispatch_kernel  -- reference moe/ref_moe.py:131-145 (for each local expert the
 //                     ascending list of tokens that selected it). One workgroup
 //                     per local expert: a histogram of all local ids gives every
@@ -23,9 +24,10 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
                                                     const uint16_t* __restrict__ bias, int T, float rsf,
                                                     int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
                                                     int32_t* __restrict__ tok_pair) {
+  __shared__ TieScratch tie[4];
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  route_token(logits, bias, t, rsf, topk_ids, topk_w, tok_pair);
+  route_token(logits, bias, t, rsf, topk_ids, topk_w, tok_pair, &tie[threadIdx.x >> 6]);
 }
 
 // One workgroup per local expert (grid = 32): each walks all T tokens in

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "moe_common.h"
+#include "moe_route_ties.h"
 
 namespace moe {
 
@@ -43,19 +44,22 @@ __device__ __forceinline__ void cx(uint32_t& ka, int& ia, uint32_t& kb, int& ib)
 //  * scores: s = 1/(1+exp(-x)) with exp(-x) evaluated in fp64 and rounded once
 //    to fp32 (the correctly rounded value), IEEE fp32 division; sb = s + bias.
 //  * group score = sum of the two largest sb of the group (multiset top-2 merged
-//    over the group's 8 lanes); a group is kept when fewer than 4 groups beat it
-//    (larger score, or equal score and lower index).
+//    over the group's 8 lanes); the 4 groups with the largest scores are kept.
 //  * the 8 experts are the 8 largest sb among the kept groups (others masked to
-//    the most negative finite float), ties to the lower id: each lane sorts its 4
-//    order-preserving keys (larger first, lower id first among equals); 8 rounds
-//    then take the wave maximum of the lanes' first keys, and the lowest lane
-//    holding it (which holds the lowest id with that key) selects that expert and
-//    drops it from its list.
+//    the most negative finite float): each lane sorts its 4 order-preserving keys
+//    (larger first); 8 rounds then take the wave maximum of the lanes' first keys,
+//    and a lane holding it selects that expert and drops it from its list.
+//  * when equal scores straddle a cut (the 4th and 5th group scores, or the 8th
+//    and 9th expert keys, are equal) the kept set is not fixed by the values
+//    alone; the reference's torch.topk(sorted=False) then keeps the entries
+//    std::nth_element leaves in front, and the wave reproduces that order
+//    (wave_nth_element) in `tie`, a 3 KB LDS scratch of its own.
 //  * weights = s / (sum of the 8 selected s + 1e-20) * rsf (unbiased s).
 // Writes, through generic pointers (global or LDS), the ascending selected ids
 // and their weights at ids[t*8 + pos], w[t*8 + pos]; tok_pair slots get -1.
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
-                                            int t, float rsf, int32_t* ids, float* wts, int32_t* tok_pair) {
+                                            int t, float rsf, int32_t* ids, float* wts, int32_t* tok_pair,
+                                            TieScratch* tie) {
   const int lane = threadIdx.x & 63;
   const float4 x4 = *reinterpret_cast<const float4*>(logits + (size_t)t * E_GLOBAL + 4 * lane);
   const uint2 b2 = *reinterpret_cast<const uint2*>(bias + 4 * lane);
@@ -86,40 +90,73 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, co
   merge(dpp_f<DPP_HALF_MIRROR>(m1), dpp_f<DPP_HALF_MIRROR>(m2));
   const float gscore = m1 + m2;
   const int g = lane >> 3;
-  int beaten = 0;
+  int above = 0, equal = 0;  // groups with a larger / the same score (this one included)
 #pragma unroll
   for (int j = 0; j < N_GROUP; ++j) {
     const float oj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), j * 8));
-    beaten += (oj > gscore || (oj == gscore && j < g)) ? 1 : 0;
+    above += oj > gscore ? 1 : 0;
+    equal += oj == gscore ? 1 : 0;
   }
-  const bool keep = beaten < TOPK_GROUP;
+  bool keep = above < TOPK_GROUP;
+  if (__ballot(above < TOPK_GROUP && above + equal > TOPK_GROUP)) {  // equal scores straddle the cut
+    VTie& s = lds_tie(tie);
+    if ((lane & 7) == 0) {
+      s.key[g] = order_key(gscore);
+      s.id[g] = (uint32_t)g;
+    }
+    wave_nth_element(s, N_GROUP, TOPK_GROUP - 1);
+    keep = false;
+#pragma unroll
+    for (int j = 0; j < TOPK_GROUP; ++j) keep |= (int)s.id[j] == g;
+  }
 
   // keys of finite floats are >= 0x00800000, so 0 marks an emptied list entry
-  uint32_t k0 = order_key(keep ? sb[0] : -3.402823466e+38f), k1 = order_key(keep ? sb[1] : -3.402823466e+38f);
-  uint32_t k2 = order_key(keep ? sb[2] : -3.402823466e+38f), k3 = order_key(keep ? sb[3] : -3.402823466e+38f);
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) key[i] = order_key(keep ? sb[i] : -3.402823466e+38f);
+  uint32_t k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
   int i0 = 0, i1 = 1, i2 = 2, i3 = 3;
   cx(k0, i0, k1, i1);
   cx(k2, i2, k3, i3);
   cx(k0, i0, k2, i2);
   cx(k1, i1, k3, i3);
   cx(k1, i1, k2, i2);
-  uint32_t selmask = 0;  // bit i: this lane's expert 4 lane + i is selected
-#pragma unroll
-  for (int r = 0; r < TOP_K; ++r) {
-    uint32_t m = k0;  // wave maximum of the lists' first keys: within rows of 16, then the 4 rows
+  // wave maximum of the lists' first keys: within rows of 16, then the 4 rows
+  auto wave_max = [&](uint32_t m) {
     m = max(m, dpp_u<DPP_XOR1>(m));
     m = max(m, dpp_u<DPP_XOR2>(m));
     m = max(m, dpp_u<DPP_HALF_MIRROR>(m));
     m = max(m, dpp_u<DPP_MIRROR>(m));
-    const uint32_t mx = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
-                            max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
-    const int win = __builtin_ctzll(__ballot(k0 == mx));  // lowest lane: lowest id with that key
+    return max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+               max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+  };
+  uint32_t selmask = 0;  // bit i: this lane's expert 4 lane + i is selected
+  uint32_t mx = 0;
+#pragma unroll
+  for (int r = 0; r < TOP_K; ++r) {
+    mx = wave_max(k0);
+    const int win = __builtin_ctzll(__ballot(k0 == mx));  // one lane holding the maximum
     if (lane == win) {
       selmask |= 1u << i0;
       k0 = k1; i0 = i1;
       k1 = k2; i1 = i2;
       k2 = k3; i2 = i3;
       k3 = 0u;
+    }
+  }
+  if (wave_max(k0) == mx) {  // the 9th largest key equals the 8th: a tie straddles the cut
+    VTie& s = lds_tie(tie);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s.key[4 * lane + i] = key[i];
+      s.id[4 * lane + i] = (uint32_t)(4 * lane + i);
+    }
+    wave_nth_element(s, E_GLOBAL, TOP_K - 1);
+    selmask = 0;
+#pragma unroll
+    for (int j = 0; j < TOP_K; ++j) {
+      const uint32_t e = s.id[j];
+      if ((int)(e >> 2) == lane) selmask |= 1u << (e & 3u);
     }
   }
   bool sel[4];

@@ -25,6 +25,7 @@
 // K block (hidden rows and gate rows, whole 128 B lines, 32-row swizzle) into a
 // 3-slot LDS ring two blocks ahead, as the prefill GEMM1 does.
 #include "moe_common.h"
+#include "moe_host.h"
 #include "moe_tile.h"
 #include "moe_quant_block.h"
 
@@ -225,13 +226,12 @@ hipError_t launch_quantize_1x128(const uint16_t* x, int T, uint8_t* q, float* sc
 
 static hipError_t launch_router_tiled(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
                                       hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(router_tiled_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, RT2_NSTAGE * RT2_STAGE);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static PerDeviceOnce<hipError_t> once;
+  hipError_t e = hipErrorInvalidDevice;
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(router_tiled_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, RT2_NSTAGE * RT2_STAGE); },
+           e);
+  if (e != hipSuccess) return e;
   const int items = (T + RT2_BM - 1) / RT2_BM * RT2_NT;
   const int grid = min((items + 7) / 8 * 8, (cu + 7) / 8 * 8);
   hipLaunchKernelGGL(router_tiled_kernel, dim3(grid), dim3(64 * (RT2_CWAVES + RT2_PWAVES)), RT2_NSTAGE * RT2_STAGE,

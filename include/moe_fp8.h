@@ -8,8 +8,8 @@
  * work is enqueued on `stream` (a hipStream_t, NULL = default stream) and
  * errors come back as negative return codes (see moe_fp8_strerror).
  * Calls on different streams are independent when each passes its own
- * workspace; the only process-global state is a per-device cache of the
- * compute-unit count and the path override below.
+ * workspace; the only process-global state is per-device set-up done once
+ * (the compute-unit count, kernel attributes), safe under concurrent callers.
  */
 #ifndef MOE_FP8_H
 #define MOE_FP8_H
@@ -27,8 +27,14 @@ enum {
   MOE_ERR_SIZE = -2,      /* T < 0 or T beyond MOE_FP8_MAX_TOKENS */
   MOE_ERR_ALIGN = -3,     /* a pointer is not 16-byte aligned */
   MOE_ERR_WORKSPACE = -4, /* workspace_bytes < moe_fp8_workspace_size(T) */
-  MOE_ERR_HIP = -5        /* a HIP launch failed; see moe_fp8_last_hip_error() */
+  MOE_ERR_HIP = -5,       /* a HIP launch failed; see moe_fp8_last_hip_error() */
+  MOE_ERR_ARG = -6        /* an enumerated argument (stage, shape) is out of range */
 };
+
+/* Kernel shape of the expert GEMMs, for the test and benchmark entry points
+ * below (moe_fp8_forward always uses MOE_SHAPE_AUTO): the decode kernels for
+ * T <= 64 and the prefill kernels above (AUTO), or the prefill kernels at any T. */
+enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
 #define MOE_FP8_MAX_TOKENS (1 << 20)
 
@@ -66,7 +72,19 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
                     void* stream);
 
 /*
- * Runs one stage of moe_fp8_forward with the same arguments, reading and
+ * moe_fp8_forward with the expert-GEMM kernel shape chosen per call (one of
+ * MOE_SHAPE_*). No reference counterpart: tests run both kernel shapes on the
+ * same inputs. Everything else as moe_fp8_forward.
+ */
+int moe_fp8_forward_shape(int shape, const float* routing_logits, const uint16_t* routing_bias,
+                          const uint8_t* hidden_states, const float* hidden_states_scale,
+                          const uint8_t* gemm1_weights, const float* gemm1_weights_scale,
+                          const uint8_t* gemm2_weights, const float* gemm2_weights_scale, int64_t T,
+                          int64_t local_expert_offset, double routed_scaling_factor, uint16_t* output,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Runs one stage of moe_fp8_forward_shape(shape, ...) with the same arguments, reading and
  * writing the workspace as the forward does: 0 = routing (+ dispatch for
  * T > 64), 1 = GEMM1 + SwiGLU (+ the in-workgroup dispatch for T <= 64),
  * 2 = GEMM2 x routing weight (+ the ordered combine for T <= 64), 3 = the
@@ -76,7 +94,7 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
  * scripts/ncu_profile.py:89-143): the benchmark times each kernel over many
  * back-to-back launches of its stage.
  */
-int moe_fp8_run_stage(int stage, const float* routing_logits, const uint16_t* routing_bias,
+int moe_fp8_run_stage(int stage, int shape, const float* routing_logits, const uint16_t* routing_bias,
                       const uint8_t* hidden_states, const float* hidden_states_scale, const uint8_t* gemm1_weights,
                       const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
                       const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
@@ -88,7 +106,9 @@ int moe_fp8_run_stage(int stage, const float* routing_logits, const uint16_t* ro
  * and top-k chain of solution/cuda/kernel_v2.cu:170-206).
  * Writes, per token, the 8 selected global expert ids in ascending order
  * (int32 [T, 8]) and their routing weights (fp32 [T, 8]). If tok_pair is not
- * NULL every one of its T*8 slots is set to -1.
+ * NULL every one of its T*8 slots is set to -1. Where equal scores straddle the
+ * group or expert cut, the kept set is the one the reference's
+ * torch.topk(sorted=False) keeps on the CPU (std::nth_element's order).
  */
 int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                   double routed_scaling_factor, int32_t* topk_ids, float* topk_w, int32_t* tok_pair,
@@ -109,14 +129,14 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
                      int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair, void* stream);
 
 /*
- * Routing and dispatch as moe_fp8_forward runs them (for T <= 64 the routing
- * kernel plus, in one workgroup, the dispatch code every decode GEMM1
- * workgroup runs; otherwise the two kernels above), writing
+ * Routing and dispatch as moe_fp8_forward_shape(shape, ...) runs them (in the
+ * decode shape the routing kernel plus, in one workgroup, the dispatch code
+ * every decode GEMM1 workgroup runs; otherwise the two kernels above), writing
  * topk_ids / topk_w [T, 8], header [128], perm_tok / perm_w [8T] and
  * tok_pair [T, 8] (fully written: -1 for non-local slots). Parity tap for
  * reference moe/ref_moe.py:94-145.
  */
-int moe_fp8_route_dispatch(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
+int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                            int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
                            float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
                            void* stream);
@@ -155,12 +175,6 @@ int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weig
  */
 int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
                             float* routing_logits, uint8_t* hidden_states, float* hidden_states_scale, void* stream);
-
-/* Kernel shape used by moe_fp8_forward: 0 = by token count (default: the
- * decode shape for T <= 64, the prefill shape above), 1 = the same as 0
- * (the decode shape exists only for T <= 64), 2 = always the prefill shape.
- * Process-global; meant for tests. Returns the previous value. */
-int moe_fp8_set_path(int path);
 
 const char* moe_fp8_strerror(int code);
 const char* moe_fp8_last_hip_error(void);

@@ -9,6 +9,9 @@ dropped bias, a transposed weight) shows up as a disagreement:
 * ``brute_force_route`` -- routing by exhaustive search: every one of the
   C(8,4) = 70 group subsets is scored and the best kept, then the 8 largest
   biased scores inside it are taken by a full sort (``ref_moe.py:94-126``).
+  Where equal scores straddle a cut the values allow several sets; the one
+  torch.topk(sorted=False) keeps is then taken from ``oracle/topk_order.py``
+  (std::nth_element's order) and checked to be one of them.
 * ``rows_fp64`` -- selected output rows recomputed in float64 from the dequantised
   operands (``ref_moe.py:67-92`` and ``:147-166``).
 """
@@ -43,25 +46,35 @@ def brute_force_route(logits: np.ndarray, bias: np.ndarray, rsf: float):
     """Per token: (sorted ids of the 8 selected experts, float64 weights in that order).
 
     ``logits`` fp32 [T,256]; ``bias`` fp32 [256] (already widened from bf16).
-    Scores are formed in float32 as the operator does; the subset search and the
-    weight normalisation run in float64.
+    Scores are formed in float32 (exp(-x) correctly rounded to float32, the
+    value torch's exp gives on the logits it is used with here); the subset
+    search and the weight normalisation run in float64. Ties at a cut are
+    resolved in torch.topk(sorted=False)'s order (``oracle/topk_order.py``).
     """
+    from oracle import topk_order
     logits = np.asarray(logits, dtype=np.float32)
     bias = np.asarray(bias, dtype=np.float32)
     one = np.float32(1.0)
-    s = one / (one + np.exp(-logits))
+    s = one / (one + np.exp(-logits.astype(np.float64)).astype(np.float32))
     sb = (s + bias).astype(np.float32)
     ids_out, w_out = [], []
     subsets = list(itertools.combinations(range(8), 4))
+    fmin = float(np.finfo(np.float32).min)
     for t in range(logits.shape[0]):
         gscore = []
         for g in range(8):
             vals = sorted(sb[t, g * 32:(g + 1) * 32].tolist(), reverse=True)
             gscore.append(float(np.float32(vals[0]) + np.float32(vals[1])))
-        best = max(subsets, key=lambda sub: (sum(gscore[g] for g in sub), [-g for g in sub]))
-        cand = [(float(sb[t, e]), -e) for g in best for e in range(g * 32, (g + 1) * 32)]
-        cand.sort(reverse=True)
-        ids = sorted(-c[1] for c in cand[:8])
+        # the best subsets by the sum of their (exact) scores: ties at the cut give several
+        score = {sub: sorted((gscore[g] for g in sub), reverse=True) for sub in subsets}
+        top = max(score.values())
+        best_sets = {frozenset(sub) for sub in subsets if score[sub] == top}
+        best = frozenset(topk_order.topk_indices(gscore, 4))
+        assert best in best_sets, "torch's group set must be one of the best subsets"
+        masked = [float(sb[t, e]) if e // 32 in best else fmin for e in range(256)]
+        cand = sorted((masked[e] for e in range(256)), reverse=True)
+        ids = sorted(topk_order.topk_indices(masked, 8))
+        assert sorted((masked[e] for e in ids), reverse=True) == cand[:8], "8 largest candidates"
         denom = sum(float(s[t, e]) for e in ids) + 1e-20
         ids_out.append(ids)
         w_out.append([float(s[t, e]) / denom * rsf for e in ids])

@@ -16,6 +16,12 @@ reference ``run`` once, and records:
 
 The fixtures are data (inputs are regenerated from seeds; expected outputs are
 stored). Usage: ``python tests/golden/make_golden.py [workload ...]``.
+
+``python tests/golden/make_golden.py ties`` writes ``ties_<case>.npz`` for the
+exact-tie routing cases of ``tests/tie_cases.py`` (selections that
+torch.topk(sorted=False)'s nth_element order decides): the logits and bias
+themselves (small), the reference's selection in its own order and sorted, and
+its bf16 output rows, with hidden states from a seeded generator.
 """
 from __future__ import annotations
 
@@ -150,5 +156,44 @@ def main(names):
         gc.collect()
 
 
+TIE_HIDDEN_SEED = 7000
+TIE_ROWS = 16
+
+
+def main_ties():
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import tie_cases as tc
+    ref = load_reference()
+    w13, s13, w2, s2 = wl.make_weights()
+    for i, name in enumerate(tc.CASES):
+        logits, bias, offset, rsf = tc.case_tensors(name)
+        T = logits.shape[0]
+        _, _, hidden, hscale = wl.make_activations(T, TIE_HIDDEN_SEED + i)
+        t0 = time.time()
+        with Capture() as cap:
+            out = ref.run(logits, bias, hidden, hscale, w13, s13, w2, s2, offset, rsf)
+        topk_idx = cap.topk[2]
+        rows = np.arange(T) if T <= TIE_ROWS else np.sort(
+            np.random.default_rng(TIE_HIDDEN_SEED + i).choice(T, TIE_ROWS, replace=False))
+        out_u16 = out.view(torch.int16).numpy().view(np.uint16)
+        np.savez_compressed(
+            os.path.join(OUT_DIR, f"ties_{name}.npz"),
+            T=T, local_expert_offset=offset, routed_scaling_factor=rsf, hidden_seed=TIE_HIDDEN_SEED + i,
+            logits=logits.numpy(), bias_bf16=bias.view(torch.int16).numpy().view(np.uint16),
+            topk_idx=topk_idx.numpy().astype(np.int16),
+            sel_ids=torch.sort(topk_idx, dim=1).values.numpy().astype(np.uint8),
+            out_rows=rows.astype(np.int32), out_bf16=out_u16[rows], out_sha256=wl.fingerprint(out),
+            in_sha256=np.array([wl.fingerprint(a) for a in (logits, bias, hidden, hscale)]),
+            torch_version=torch.__version__,
+            cpu_capability=torch.backends.cpu.get_cpu_capability(),
+        )
+        print(f"ties_{name}: T={T} offset={offset} ref_run={time.time() - t0:.1f}s", flush=True)
+        del out, cap
+        gc.collect()
+
+
 if __name__ == "__main__":
-    main(sys.argv[1:] or list(wl.WORKLOADS))
+    if sys.argv[1:] == ["ties"]:
+        main_ties()
+    else:
+        main(sys.argv[1:] or list(wl.WORKLOADS))

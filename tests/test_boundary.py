@@ -37,8 +37,8 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.moe_fp8_abi_version() == 1
-    for code in (0, -1, -2, -3, -4, -5):
+    assert lib.moe_fp8_abi_version() == 2
+    for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.moe_fp8_strerror(code)
     assert lib.moe_fp8_strerror(-99) == b"unknown error"
 
@@ -121,10 +121,21 @@ def test_router_quantize_argument_errors(lib):
         assert r(args[0], args[1], 4, args[2], args[3], args[4], None) == _lib.MOE_ERR_ALIGN, i
 
 
-def test_set_path(lib):
-    assert lib.moe_fp8_set_path(7) == -1
-    old = lib.moe_fp8_set_path(2)
-    assert lib.moe_fp8_set_path(old) == 2
+def test_shape_argument(lib):
+    """The kernel shape is a per-call argument of the test and bench entry points
+    (there is no process-global switch); out-of-range values are rejected first."""
+    assert not hasattr(_lib.SIGNATURES, "moe_fp8_set_path") and "moe_fp8_set_path" not in _lib.SIGNATURES
+    args = [FAKE] * 8 + [1, 0, 2.5, FAKE, FAKE, 1 << 40, None]
+    for bad in (-1, 2, 7):
+        assert lib.moe_fp8_forward_shape(bad, *args) == _lib.MOE_ERR_ARG
+        assert lib.moe_fp8_run_stage(0, bad, *args) == _lib.MOE_ERR_ARG
+        assert lib.moe_fp8_route_dispatch(bad, FAKE, FAKE, 4, 0, 2.5, *[FAKE] * 6, None) == _lib.MOE_ERR_ARG
+    for stage in (-1, 4):
+        assert lib.moe_fp8_run_stage(stage, 0, *args) == _lib.MOE_ERR_ARG
+    for shape in (_lib.MOE_SHAPE_AUTO, _lib.MOE_SHAPE_PREFILL):  # valid shape: the usual checks follow
+        assert lib.moe_fp8_forward_shape(shape, *[FAKE] * 8, -1, 0, 2.5, FAKE, FAKE, 1 << 40, None) == \
+            _lib.MOE_ERR_SIZE
+        assert lib.moe_fp8_forward_shape(shape, *[FAKE] * 8, 0, 0, 2.5, FAKE, FAKE, 1 << 40, None) == _lib.MOE_OK
 
 
 def _cpu_inputs(T=2):
