@@ -18,6 +18,8 @@ MOE_ERR_ALIGN = -3
 MOE_ERR_WORKSPACE = -4
 MOE_ERR_HIP = -5
 MOE_ERR_ARG = -6
+MOE_ERR_NOALLOC_SIZE = -7
+MOE_FP8_NOALLOC_MAX_TOKENS = 64
 
 MOE_SHAPE_AUTO = 0
 MOE_SHAPE_PREFILL = 1
@@ -29,6 +31,8 @@ SIGNATURES = {
     "moe_fp8_workspace_size": (ctypes.c_size_t, [_I64]),
     "moe_fp8_forward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double, _P, _P,
                                        ctypes.c_size_t, _P]),
+    "moe_fp8_forward_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, ctypes.c_double, _P,
+                                               _P]),
     "moe_fp8_forward_shape": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                              ctypes.c_double, _P, _P, ctypes.c_size_t, _P]),
     "moe_fp8_run_stage": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,

@@ -4,6 +4,7 @@
 // GEMM2 x weight -> ordered combine (inside GEMM2 in the decode shape). No host
 // synchronisation, no allocation.
 #include "moe_common.h"
+#include "moe_host.h"
 #include "../../include/moe_fp8.h"
 
 #include <algorithm>
@@ -109,7 +110,8 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
       !aligned16(hidden_states_scale) || !aligned16(gemm1_weights) || !aligned16(gemm1_weights_scale) ||
       !aligned16(gemm2_weights) || !aligned16(gemm2_weights_scale) || !aligned16(output) || !aligned16(workspace))
     return MOE_ERR_ALIGN;
-  const WorkspaceLayout L = WorkspaceLayout::make(T);
+  const bool decode = shape == MOE_SHAPE_AUTO && T <= kDecodeMaxTokens;
+  const WorkspaceLayout L = WorkspaceLayout::make(T, !decode);  // the decode kernels use no partial rows
   if (workspace_bytes < L.total) return MOE_ERR_WORKSPACE;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   c.logits = routing_logits;
@@ -124,7 +126,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   c.offset = clamp_offset(local_expert_offset);
   c.rsf = (float)routed_scaling_factor;
   c.out = output;
-  c.decode = shape == MOE_SHAPE_AUTO && T <= kDecodeMaxTokens;
+  c.decode = decode;
   c.stream = reinterpret_cast<hipStream_t>(stream);
   c.hdr = reinterpret_cast<DispatchHeader*>(ws + L.hdr);
   c.topk_ids = reinterpret_cast<int32_t*>(ws + L.topk_ids);
@@ -325,6 +327,61 @@ int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_we
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward for decode sizes: the workspace is a file-scope
+// device array (each device holds its own copy, for the life of the process),
+// addressed through the pointer hipGetSymbolAddress returns on that device.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = moe::WorkspaceLayout::make(MOE_FP8_NOALLOC_MAX_TOKENS, false).total;
+static_assert(kNoAllocScratchBytes < (4u << 20), "a modest scratch: header, ids, permutation and bf16 C rows");
+
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+struct ScratchAddress {
+  hipError_t err = hipErrorInvalidDevice;
+  void* ptr = nullptr;
+};
+moe::PerDeviceOnce<ScratchAddress> g_scratch;
+
+// The current device's copy of `scratch`, looked up once per device.
+int scratch_address(void** out) {
+  ScratchAddress a;
+  if (!g_scratch.get([] {
+        ScratchAddress r;
+        r.err = hipGetSymbolAddress(&r.ptr, HIP_SYMBOL(scratch));
+        return r;
+      }, a))
+    return hip_fail(hipErrorInvalidDevice);
+  if (a.err != hipSuccess) return hip_fail(a.err);
+  if (a.ptr == nullptr) return hip_fail(hipErrorInvalidSymbol);
+  *out = a.ptr;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_fp8_forward_noalloc(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                            const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                            const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                            const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                            double routed_scaling_factor, uint16_t* output, void* stream) {
+  if (T < 0) return MOE_ERR_SIZE;
+  if (T > MOE_FP8_NOALLOC_MAX_TOKENS) return MOE_ERR_NOALLOC_SIZE;
+  if (T == 0) return MOE_OK;
+  void* ws = nullptr;
+  const int r = scratch_address(&ws);
+  if (r != MOE_OK) return r;
+  return forward(MOE_SHAPE_AUTO, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                 gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
+                 routed_scaling_factor, output, ws, kNoAllocScratchBytes, stream);
+}
+
 const char* moe_fp8_strerror(int code) {
   switch (code) {
     case MOE_OK: return "ok";
@@ -334,6 +391,8 @@ const char* moe_fp8_strerror(int code) {
     case MOE_ERR_WORKSPACE: return "workspace smaller than moe_fp8_workspace_size(T)";
     case MOE_ERR_HIP: return "HIP launch failed";
     case MOE_ERR_ARG: return "an enumerated argument (stage, shape) is out of range";
+    case MOE_ERR_NOALLOC_SIZE:
+      return "token count beyond MOE_FP8_NOALLOC_MAX_TOKENS (64) for moe_fp8_forward_noalloc; use moe_fp8_forward";
     default: return "unknown error";
   }
 }

@@ -91,10 +91,13 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 
 __host__ __device__ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Workspace layout for T tokens (worst case P = 8T routed pairs).
+// Workspace layout for T tokens (worst case P = 8T routed pairs). The fp32
+// partial rows come last: only the prefill kernels use them, so a decode-shape
+// call needs `total` bytes of make(T, false) (the same offsets, no partial rows).
 struct WorkspaceLayout {
-  size_t hdr, topk_ids, topk_w, tok_pair, perm_tok, perm_w, c_act, partial, total;
-  __host__ __device__ static WorkspaceLayout make(int64_t T) {
+  size_t hdr = 0, topk_ids = 0, topk_w = 0, tok_pair = 0, perm_tok = 0, perm_w = 0, c_act = 0, partial = 0,
+         total = 0;
+  __host__ __device__ static constexpr WorkspaceLayout make(int64_t T, bool with_partial = true) {
     WorkspaceLayout L;
     const size_t P = (size_t)T * TOP_K;
     size_t o = 0;
@@ -105,7 +108,7 @@ struct WorkspaceLayout {
     L.perm_tok = o; o += align_up(P * 4, 256);
     L.perm_w = o;   o += align_up(P * 4, 256);
     L.c_act = o;    o += align_up(P * I * 2, 256);
-    L.partial = o;  o += align_up(P * H * 4, 256);
+    L.partial = o;  o += with_partial ? align_up(P * H * 4, 256) : 0;
     L.total = o;
     return L;
   }

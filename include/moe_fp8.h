@@ -28,7 +28,8 @@ enum {
   MOE_ERR_ALIGN = -3,     /* a pointer is not 16-byte aligned */
   MOE_ERR_WORKSPACE = -4, /* workspace_bytes < moe_fp8_workspace_size(T) */
   MOE_ERR_HIP = -5,       /* a HIP launch failed; see moe_fp8_last_hip_error() */
-  MOE_ERR_ARG = -6        /* an enumerated argument (stage, shape) is out of range */
+  MOE_ERR_ARG = -6,       /* an enumerated argument (stage, shape) is out of range */
+  MOE_ERR_NOALLOC_SIZE = -7 /* T beyond MOE_FP8_NOALLOC_MAX_TOKENS in moe_fp8_forward_noalloc */
 };
 
 /* Kernel shape of the expert GEMMs, for the test and benchmark entry points
@@ -70,6 +71,26 @@ int moe_fp8_forward(const float* routing_logits, const uint16_t* routing_bias, c
                     const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
                     double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/*
+ * moe_fp8_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation). No counterpart in the reference. The workspace is a
+ * library-owned device array of about 2.1 MB that each GPU holds from the first
+ * call on it until the process ends; nothing here allocates. Limits:
+ *   - T <= MOE_FP8_NOALLOC_MAX_TOKENS (64, the decode kernels); larger T returns
+ *     MOE_ERR_NOALLOC_SIZE (use moe_fp8_forward with a workspace);
+ *   - every call on one GPU shares that GPU's array: calls that overlap on one
+ *     GPU (e.g. on two streams without ordering between them) race and give
+ *     wrong results; order them on one stream.
+ * Results are bit-identical to moe_fp8_forward's on the same inputs.
+ */
+#define MOE_FP8_NOALLOC_MAX_TOKENS 64
+int moe_fp8_forward_noalloc(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
+                            const float* hidden_states_scale, const uint8_t* gemm1_weights,
+                            const float* gemm1_weights_scale, const uint8_t* gemm2_weights,
+                            const float* gemm2_weights_scale, int64_t T, int64_t local_expert_offset,
+                            double routed_scaling_factor, uint16_t* output, void* stream);
 
 /*
  * moe_fp8_forward with the expert-GEMM kernel shape chosen per call (one of

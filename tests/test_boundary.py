@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(lib):
 
 def test_abi_version_and_strings(lib):
     assert lib.moe_fp8_abi_version() == 2
-    for code in (0, -1, -2, -3, -4, -5, -6):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7):
         assert lib.moe_fp8_strerror(code)
     assert lib.moe_fp8_strerror(-99) == b"unknown error"
 
@@ -74,7 +74,22 @@ def test_forward_argument_errors(lib):
     ptrs = [FAKE] * 8
     ptrs[4] = FAKE + 4
     assert _fwd(lib, ptrs=ptrs) == _lib.MOE_ERR_ALIGN
-    assert _fwd(lib, T=16, ws_bytes=lib.moe_fp8_workspace_size(16) - 1) == _lib.MOE_ERR_WORKSPACE
+    # the prefill kernels need the whole moe_fp8_workspace_size(T)
+    assert _fwd(lib, T=100, ws_bytes=lib.moe_fp8_workspace_size(100) - 1) == _lib.MOE_ERR_WORKSPACE
+    assert lib.moe_fp8_forward_shape(_lib.MOE_SHAPE_PREFILL, *[FAKE] * 8, 16, 0, 2.5, FAKE, FAKE,
+                                     lib.moe_fp8_workspace_size(16) - 1, None) == _lib.MOE_ERR_WORKSPACE
+    # the decode kernels (T <= 64) use no fp32 partial rows: less is enough, but not a few bytes
+    assert _fwd(lib, T=16, ws_bytes=4096) == _lib.MOE_ERR_WORKSPACE
+
+
+def test_noalloc_argument_errors(lib):
+    """Rejected on the host before any GPU call: beyond its 64-token limit, T < 0."""
+    f = lib.moe_fp8_forward_noalloc
+    assert f(*[FAKE] * 8, 65, 0, 2.5, FAKE, None) == _lib.MOE_ERR_NOALLOC_SIZE
+    assert f(*[FAKE] * 8, 1 << 20, 0, 2.5, FAKE, None) == _lib.MOE_ERR_NOALLOC_SIZE
+    assert f(*[FAKE] * 8, -1, 0, 2.5, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert f(*[FAKE] * 8, 0, 0, 2.5, FAKE, None) == _lib.MOE_OK
+    assert lib.moe_fp8_strerror(_lib.MOE_ERR_NOALLOC_SIZE).startswith(b"token count beyond")
 
 
 def test_route_and_dispatch_argument_errors(lib):
