@@ -10,15 +10,21 @@ Printed JSON line (rank 0, one line):
   value         tokens/s over the sweep = steps * sum(T) / wall time of the timed steps
                 (the step timed as a HIP graph replay and as plain API calls; the faster)
   ms_per_step   wall time of one sweep
-  per_T         us/call (back-to-back calls), tokens/s, op-level HBM fraction, the cold
-                (MALL flushed) call time and each stage's kernel time per T
+  per_T         us/call (the reference harness's protocol, scripts/run_local.py:33:
+                3 warmup calls, then 5 trials of 100 back-to-back calls, median of the
+                trials' means), tokens/s, op-level HBM fraction, the cold (MALL flushed)
+                call time and each stage's kernel time per T (null: the stage launches
+                nothing at that T)
   roofline      the dominant kernel (GEMM1 weight streaming): algorithmic bytes per
                 launch / its mean duration (many back-to-back launches of that stage
                 between two HIP events on the operator's stream), against 8 TB/s
   cpu_baseline  the CPU oracle (PyTorch restatement of the reference, all 32 experts
                 dequantised per call as the reference does) timed on this host
-  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096) and the
-                producer-side kernels (FP8 activation quantiser, router GEMM, both fused) at T = 64 and 8192
+  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096), each with
+                a roofline object against its binding roof (HBM bytes / 8 TB/s or e4m3 GEMM1 at
+                5.0 PFLOP/s + bf16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; the drop-in
+                Python entry point timed at T=1 (host cost included); and the producer-side
+                kernels (FP8 activation quantiser, router GEMM, both fused) at T = 64 and 8192
 """
 from __future__ import annotations
 
@@ -44,6 +50,8 @@ HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0   # dense e4m3 MFMA
 BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 STAGES = ["route_dispatch", "gemm1", "gemm2", "combine"]
+# the reference harness's timing protocol (scripts/run_local.py:33: BenchmarkConfig)
+HARNESS_WARMUP, HARNESS_ITERS, HARNESS_TRIALS = 3, 100, 5
 
 W13_BYTES = 2 * wl.I * wl.H + wl.NB_G1 * wl.NB_H * 4     # one expert's fp8 W13 + its scales
 W2_BYTES = wl.H * wl.I + wl.NB_H * wl.NB_I * 4
@@ -114,16 +122,38 @@ class Runner:
         return self.ev[0].elapsed_time(self.ev[1]) / reps * 1e3
 
     def stage_us(self, c: Case, reps: int):
-        """Mean duration of each stage's kernel(s): a graph of `reps` back-to-back launches of that stage."""
+        """Mean duration of each stage's kernel(s): a graph of `reps` back-to-back launches of that
+        stage; None for a stage that launches nothing at this T (routing at T <= 8, which the
+        decode GEMM1 does itself; the combine at T <= 64, done inside the decode GEMM2)."""
         self.call(c)
         out = []
         for s in range(4):
+            if (s == 0 and c.T <= 8) or (s == 3 and c.T <= 64):
+                out.append(None)
+                continue
             g = self.graph(lambda: self.stage(c, s), reps)
             out.append(self.graph_us(g, reps))
             del g
         self.call(c)  # leave the workspace and output consistent
         torch.cuda.synchronize()
         return out
+
+    def harness_us(self, fn):
+        """The reference harness's protocol: HARNESS_WARMUP untimed calls, then HARNESS_TRIALS
+        trials of HARNESS_ITERS back-to-back calls between two HIP events on the operator's
+        stream; returns (median of the trials' per-call means, all trial means) in us."""
+        for _ in range(HARNESS_WARMUP):
+            fn()
+        torch.cuda.synchronize()
+        trials = []
+        for _ in range(HARNESS_TRIALS):
+            self.ev[0].record()
+            for _ in range(HARNESS_ITERS):
+                fn()
+            self.ev[1].record()
+            torch.cuda.synchronize()
+            trials.append(self.ev[0].elapsed_time(self.ev[1]) / HARNESS_ITERS * 1e3)
+        return statistics.median(trials), trials
 
     def cold_us(self, c: Case, reps: int, flush, sink):
         """Median us of one call after reading a 1 GiB buffer (4x the 256 MB MALL).
@@ -150,20 +180,13 @@ def check_against_golden(c: Case):
         return None
     with np.load(path, allow_pickle=False) as g:
         rows, ref_bits = g["out_rows"], g["out_bf16"]
-    got = c.out.float().cpu().numpy()[rows]
-    ref = (ref_bits.astype(np.uint32) << 16).view(np.float32)
-    bad = np.abs(got - ref) > 1e-2 + 2e-2 * np.abs(ref)
-    if bad.any():
-        raise SystemExit(f"[bench] {c.name}: output differs from the reference ({int(bad.sum())} elements)")
-    return True
-
-
-def time_plain(runner, c: Case, reps):
-    """GPU us per call: a graph of `reps` back-to-back calls, replayed between two events."""
-    g = runner.graph(lambda: runner.call(c), reps)
-    us = runner.graph_us(g, reps)
-    del g
-    return us
+    got = c.out.float().cpu().numpy()[rows].astype(np.float64)
+    ref = (ref_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    ratio = np.abs(got - ref) / (1e-2 + 2e-2 * np.abs(ref))
+    if (ratio > 1).any():
+        raise SystemExit(f"[bench] {c.name}: output differs from the reference ({int((ratio > 1).sum())} elements)")
+    return {"rows": int(len(rows)), "max_abs_error": float(np.abs(got - ref).max()),
+            "max_err_over_bar": round(float(ratio.max()), 4)}
 
 
 def cpu_baseline(sweep_names):
@@ -192,6 +215,30 @@ def cpu_baseline(sweep_names):
         "cpu_model": _cpu_model(),
         "torch": torch.__version__,
     }
+
+
+def cpu_oracle_us(name):
+    """One timed call of the oracle on the host CPU for a configuration (the reference's own
+    per-workload CPU figure; BASELINE's path 2: one call for T >= 1024)."""
+    from oracle import cpu_ref  # only the CPU-baseline leg uses the oracle
+    w = wl.WORKLOADS[name]
+    w13, s13, w2, s2 = wl.make_weights()
+    acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    t0 = time.perf_counter()
+    cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor, materialize_all=True)
+    return (time.perf_counter() - t0) * 1e6
+
+
+def binding_roofline(c, us):
+    """The configuration's binding roof: HBM (algorithmic bytes at 8 TB/s) or MFMA (GEMM1 on the
+    e4m3 MFMA at 5.0 PFLOP/s plus GEMM2 on the bf16 MFMA at 2.5 PFLOP/s), whichever is slower."""
+    hbm_us = c.bytes / (HBM_PEAK_GBS * 1e9) * 1e6
+    mfma_us = (c.P * GEMM1_FLOPS_PER_PAIR / (FP8_PEAK_TFLOPS * 1e12)
+               + c.P * GEMM2_FLOPS_PER_PAIR / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
+    bound = "hbm" if hbm_us >= mfma_us else "mfma"
+    floor = max(hbm_us, mfma_us)
+    return {"bound": bound, "floor_us": round(floor, 1), "hbm_floor_us": round(hbm_us, 1),
+            "mfma_floor_us": round(mfma_us, 1), "achieved_us": round(us, 1), "frac": round(floor / us, 4)}
 
 
 def _cpu_model():
@@ -294,15 +341,17 @@ def main():
     cases = {n: Case(n, dev, weights_gpu) for n in sweep + extra}
     runner = Runner(dev, max(c.T for c in cases.values()))
 
+    accuracy = {}
     for c in cases.values():
         runner.call(c)
         torch.cuda.synchronize()
-        check_against_golden(c)
+        accuracy[c.name] = check_against_golden(c)
         for stage in range(4):  # the per-stage path must reproduce the forward's output
             runner.stage(c, stage)
         torch.cuda.synchronize()
         check_against_golden(c)
-    log("outputs match the reference rows")
+    log("outputs match the reference rows: worst |err| / (atol + rtol |ref|) per config "
+        + ", ".join(f"{n} {a['max_err_over_bar']}" for n, a in accuracy.items() if a))
 
     # --- headline: K timed sweeps, wall clock bracketed by synchronize -------------
     # One step = one call at each T of the sweep. It is timed both ways a caller
@@ -350,23 +399,28 @@ def main():
     flush = torch.zeros((4096, (1 << 30) // 4 // 4096), dtype=torch.float32, device=dev)  # 1 GiB, 4x the MALL
     sink = torch.empty(4096, dtype=torch.float32, device=dev)
     per_T, g1_bytes, g1_us = [], [], []
+    def r2(v):
+        return None if v is None else round(v, 2)
+
     for c in sweep_cases:
-        plain = time_plain(runner, c, args.reps)
+        plain, trials = runner.harness_us(lambda: runner.call(c))
         st = runner.stage_us(c, args.reps)
         cold = runner.cold_us(c, max(5, args.reps // 3), flush, sink)
         g1_bytes.append(c.gemm1_bytes)
         g1_us.append(st[1])
         per_T.append({
             "T": c.T, "P": c.P, "E_act": c.E_act,
-            "us_per_call": round(plain, 2), "tokens_per_s": round(c.T / (plain * 1e-6), 1),
+            "us_per_call": round(plain, 2), "trials_us": [round(t, 2) for t in trials],
+            "tokens_per_s": round(c.T / (plain * 1e-6), 1),
             "hbm_frac": round(c.bytes / (plain * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
             "cold_us_per_call": round(cold, 2),
             "cold_hbm_frac": round(c.bytes / (cold * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
-            "stage_us": {k: round(v, 2) for k, v in zip(STAGES, st)},
+            "stage_us": {k: r2(v) for k, v in zip(STAGES, st)},
+            "accuracy_vs_reference_rows": accuracy.get(c.name),
             "gemm1_hbm_frac": round(c.gemm1_bytes / (st[1] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
             "gemm2_hbm_frac": round(c.gemm2_bytes / (st[2] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
         })
-        log(f"T={c.T}: {plain:.1f} us/call, stages {[round(x, 1) for x in st]}")
+        log(f"T={c.T}: {plain:.1f} us/call, stages {[r2(x) for x in st]}")
     del flush, sink
     mean_bytes = statistics.fmean(g1_bytes)
     mean_us = statistics.fmean(g1_us)
@@ -388,19 +442,45 @@ def main():
     for n in extra:
         c = cases[n]
         reps = 5 if c.T >= 4096 else args.reps // 2
-        plain = time_plain(runner, c, reps)
+        plain, trials = runner.harness_us(lambda: runner.call(c))
         st = runner.stage_us(c, reps)
         t_s = plain * 1e-6
         also[n] = {
             "T": c.T, "P": c.P, "E_act": c.E_act, "us_per_call": round(plain, 1),
+            "trials_us": [round(t, 1) for t in trials],
             "tokens_per_s": round(c.T / t_s, 1),
+            "roofline": binding_roofline(c, plain),
             "mfma_frac_fp8_peak": round(c.flops / t_s / (FP8_PEAK_TFLOPS * 1e12), 4),
             "hbm_frac": round(c.bytes / t_s / (HBM_PEAK_GBS * 1e9), 4),
-            "stage_us": {k: round(v, 1) for k, v in zip(STAGES, st)},
+            "stage_us": {k: r2(v) for k, v in zip(STAGES, st)},
             "gemm1_tflops": round(c.P * GEMM1_FLOPS_PER_PAIR / (st[1] * 1e-6) / 1e12, 1),
             "gemm2_tflops": round(c.P * GEMM2_FLOPS_PER_PAIR / (st[2] * 1e-6) / 1e12, 1),
+            "accuracy_vs_reference_rows": accuracy.get(n),
         }
-        log(f"{n}: {also[n]['us_per_call']} us/call, stages {[round(x, 1) for x in st]}")
+        log(f"{n}: {also[n]['us_per_call']} us/call ({also[n]['roofline']['frac']} of the "
+            f"{also[n]['roofline']['bound']} roof), stages {[r2(x) for x in st]}")
+    # every sweep T against its own (HBM) roof as well
+    for row, c in zip(per_T, sweep_cases):
+        row["roofline"] = binding_roofline(c, row["us_per_call"])
+
+    # the drop-in Python entry point at T=1: validation, workspace from torch's allocator and
+    # the ctypes call included (host wall clock per call over back-to-back calls)
+    c1 = cases["decode_t1"]
+    out1 = torch.empty_like(c1.out)
+    dropin = lambda: fm.kernel(*c1.args, c1.offset, c1.rsf, out1)  # noqa: E731
+    gpu_us, _ = runner.harness_us(dropin)
+    for _ in range(HARNESS_WARMUP):
+        dropin()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(HARNESS_ITERS):
+        dropin()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) / HARNESS_ITERS * 1e6
+    also["dropin_kernel_T1"] = {"us_per_call_gpu_events": round(gpu_us, 2), "us_per_call_wall": round(wall_us, 2),
+                                "c_abi_us_per_call": per_T[0]["us_per_call"]}
+    log(f"fm.kernel T=1: {wall_us:.1f} us wall per call, {gpu_us:.1f} us between events "
+        f"(C ABI: {per_T[0]['us_per_call']} us)")
 
     # the producer-side activation quantiser (bf16 -> e4m3 + [56, T] scales), HBM-bound
     if not args.no_extra:
@@ -459,6 +539,11 @@ def main():
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         cpu = cpu_baseline(sweep)
+        for n in extra:  # one timed oracle call per other configuration
+            us = cpu_oracle_us(n)
+            also[n]["cpu_oracle_us_per_call"] = round(us, 1)
+            also[n]["gpu_speedup_vs_cpu_oracle"] = round(us / also[n]["us_per_call"], 1)
+            log(f"CPU oracle {n}: {us / 1e6:.2f} s")
 
     out = {
         "metric": METRIC,
