@@ -20,7 +20,8 @@ Printed JSON line (rank 0, one line):
                 between two HIP events on the operator's stream), against 8 TB/s
   cpu_baseline  the CPU oracle (PyTorch restatement of the reference, all 32 experts
                 dequantised per call as the reference does) timed on this host
-  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096), each with
+  also          the other benchmark configurations (prefill 1024 / 8192, skew 4096, and the two
+                largest official token counts 11,948 / 14,107 with their bias profile), each with
                 a roofline object against its binding roof (HBM bytes / 8 TB/s or e4m3 GEMM1 at
                 5.0 PFLOP/s + bf16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; the drop-in
                 Python entry point timed at T=1 (host cost included); and the producer-side
@@ -69,7 +70,7 @@ class Case:
     def __init__(self, name, dev, weights_gpu):
         w = wl.WORKLOADS[name]
         self.name, self.T, self.offset, self.rsf = name, w.T, w.local_expert_offset, w.routed_scaling_factor
-        acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+        acts = wl.workload_activations(w)
         self.args = [a.to(dev) for a in acts] + list(weights_gpu)
         self.out = torch.empty((w.T, wl.H), dtype=torch.bfloat16, device=dev)
         ids, wts, pair = fm.route(self.args[0], self.args[1], self.rsf)
@@ -197,7 +198,7 @@ def cpu_baseline(sweep_names):
     tot_t, tot_tok = 0.0, 0
     for name in sweep_names:
         w = wl.WORKLOADS[name]
-        acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+        acts = wl.workload_activations(w)
         t0 = time.perf_counter()
         cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor, materialize_all=True)
         tot_t += time.perf_counter() - t0
@@ -223,7 +224,7 @@ def cpu_oracle_us(name):
     from oracle import cpu_ref  # only the CPU-baseline leg uses the oracle
     w = wl.WORKLOADS[name]
     w13, s13, w2, s2 = wl.make_weights()
-    acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    acts = wl.workload_activations(w)
     t0 = time.perf_counter()
     cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor, materialize_all=True)
     return (time.perf_counter() - t0) * 1e6
@@ -337,7 +338,8 @@ def main():
     if args.mfma_pass:
         mfma_pass(dev, weights_gpu, args.reps)
         return
-    extra = [] if args.no_extra else ["t16", "prefill_t1024", "prefill_t8192", "skew_t4096"]
+    extra = [] if args.no_extra else ["t16", "prefill_t1024", "prefill_t8192", "skew_t4096", "trace_t11948",
+                                      "trace_t14107"]
     cases = {n: Case(n, dev, weights_gpu) for n in sweep + extra}
     runner = Runner(dev, max(c.T for c in cases.values()))
 

@@ -27,6 +27,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // Device-side dispatch header at the start of the workspace.
 struct DispatchHeader {
@@ -53,22 +55,35 @@ __device__ __forceinline__ v4f mfma_bf16_k32(const v8bf& a, const v8bf& b, const
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Four e4m3 codes (one dword) -> four bf16 packed in two dwords. e4m3 values
-// are exact in fp32 and in bf16 (3 mantissa bits), so taking the upper half of
-// the fp32 pattern is exact.
-template <bool HI>
-__device__ __forceinline__ v2f fp8x2_to_f32(uint32_t w) {
-  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+// D += A(16x32 fp16) * B(32x16 fp16); the same lane layout as mfma_bf16_k32.
+__device__ __forceinline__ v4f mfma_f16_k32(const v8h& a, const v8h& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ uint32_t pack_bf16_hi(float lo, float hi) {
-  // byte select: result = {hi[31:16], lo[31:16]}
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+
+// Eight e4m3 codes (two dwords) -> eight fp16 in K order, exactly: every e4m3 value
+// (at most 448 in magnitude, subnormals down to 2^-9) is an fp16 value.
+// v_cvt_scalef32_pk_f16_fp8 with scale 1.0 converts the two codes of one 16-bit half
+// (checked on the GPU against the OCP table for all 256 codes in all 4 byte positions).
+__device__ __forceinline__ v8h fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
+  const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const v2h b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const v2h c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const v2h d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return v8h{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
-__device__ __forceinline__ void fp8x4_to_bf16x4(uint32_t w, uint32_t& o0, uint32_t& o1) {
-  v2f a = fp8x2_to_f32<false>(w);
-  v2f b = fp8x2_to_f32<true>(w);
-  o0 = pack_bf16_hi(a[0], a[1]);
-  o1 = pack_bf16_hi(b[0], b[1]);
+
+// The SwiGLU output C (the GEMM2 activation operand) is stored as fp16 of C * 2^-8:
+// 11 significant bits for |C| in [2^-6, 2^24) and an absolute step of 2^-24 * 2^8
+// below (bf16 keeps 8 bits, and its rounding of C moved a few outputs of a skewed
+// routing past the 1e-2 / 2e-2 bar through cancellation across experts). Values
+// beyond the fp16 range saturate to +-65504 * 2^8; NaN stays NaN. GEMM2 multiplies
+// its fp32 accumulators by 2^8 together with the weight block scale.
+constexpr float C_STORE_SCALE = 1.0f / 256.0f;
+constexpr float C_LOAD_SCALE = 256.0f;
+__device__ __forceinline__ uint16_t c_encode(float c) {
+  const float x = c * C_STORE_SCALE;  // exact: a power of two
+  const float y = x != x ? x : fminf(fmaxf(x, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)y);  // round to nearest even
 }
 
 // Barrier for LDS traffic only. __syncthreads() also orders global memory, and

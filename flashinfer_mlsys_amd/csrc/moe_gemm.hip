@@ -11,8 +11,9 @@
 // GEMM1 runs on the e4m3 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
 // scales). One MFMA covers exactly one 128-wide K block, so the fp32 block
 // scales are applied once per block: acc += P * (s_act[row, kb] * s_w[nb, kb]).
-// GEMM2 runs on the bf16 MFMA: e4m3 weights widen to bf16 exactly; the bf16 C
-// keeps the SwiGLU output to 8 significant bits.
+// GEMM2 runs on the fp16 MFMA: e4m3 weights widen to fp16 exactly, and C is
+// stored as fp16 of C * 2^-8 (c_encode: 11 significant bits), the 2^8 going back
+// in with the weight block scale.
 //
 // Two shapes of each GEMM:
 //   *_decode  -- T <= 64, few rows per expert, weight-streaming bound. The
@@ -44,16 +45,6 @@ __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
   r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
   return r;
-}
-
-// 8 e4m3 codes (two dwords) -> 8 bf16 in K order.
-__device__ __forceinline__ v8bf fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-  v4i r;
-  uint32_t a, b, c, d;
-  fp8x4_to_bf16x4(w0, a, b);
-  fp8x4_to_bf16x4(w1, c, d);
-  r[0] = (int)a; r[1] = (int)b; r[2] = (int)c; r[3] = (int)d;
-  return __builtin_bit_cast(v8bf, r);
 }
 
 __device__ __forceinline__ float silu_mul(float x1, float x2) {
@@ -327,7 +318,7 @@ __device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i
           x2 += red[w][r][ln + 8];
         }
         const int row = m0 + 4 * (ln >> 4) + r;
-        if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = f32_to_bf16_rne(silu_mul(x1, x2));
+        if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = c_encode(silu_mul(x1, x2));
       }
     }
     ++st.phase;
@@ -417,10 +408,10 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
 // Workgroup c owns output columns 28 c .. 28 c + 27 (W2 rows; 256 workgroups
 // cover H = 7168 exactly, so every workgroup streams the same weight bytes) and
 // takes every active expert in ascending id: one item per expert, 28 W2 rows x
-// 2048 as two column blocks of the bf16 16x16x32 MFMA (the second block's last
+// 2048 as two column blocks of the fp16 16x16x32 MFMA (the second block's last
 // 4 columns repeat row 27 and are dropped). Each of the 8 waves owns 2 of the 16
 // K blocks. Lane (fr, kg) reads 32 contiguous e4m3 bytes of a W2 row per K block
-// and the same 32 K values (bf16, 64 B) of its activation row, so step j of a
+// and the same 32 K values (fp16, 64 B) of its activation row, so step j of a
 // block takes K 32 kg + 8 j + [0, 8) in both operands. Weights stream through a
 // 3-deep register ring (items i+1 and i+2 in flight while item i computes); the
 // activation rows of item i+1 (the next expert's first 16 pairs) are loaded into
@@ -472,7 +463,7 @@ __device__ __forceinline__ void g2_load_w(v4i (&b)[D2_LD], const uint8_t* __rest
   }
 }
 
-// This wave's K slice (2 K blocks of bf16 activations) of pair rows m0 .. m0 + 15
+// This wave's K slice (2 K blocks of fp16 activations) of pair rows m0 .. m0 + 15
 // of an expert's segment (rows past cnt repeat the last one), in MFMA operand order.
 struct G2A {
   v4i q[D2_KPW][4];
@@ -504,7 +495,7 @@ __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b
   float sw[2][D2_KPW];
 #pragma unroll
   for (int kk = 0; kk < D2_KPW; ++kk) {
-    const float lo = sp[blo * NB_I + kk], hi = sp[bhi * NB_I + kk];
+    const float lo = sp[blo * NB_I + kk] * C_LOAD_SCALE, hi = sp[bhi * NB_I + kk] * C_LOAD_SCALE;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) sw[cb][kk] = (c0 + min(cb * 16 + fr, D2_COLS - 1)) / BLK == blo ? lo : hi;
   }
@@ -527,8 +518,8 @@ __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const v4i wq = b[(cb * D2_KPW + kk) * 2 + (j >> 1)];
-          const v8bf wb = fp8x8_to_bf16x8((uint32_t)wq[2 * (j & 1)], (uint32_t)wq[2 * (j & 1) + 1]);
-          p = mfma_bf16_k32(__builtin_bit_cast(v8bf, cur.q[kk][j]), wb, p);
+          const v8h wb = fp8x8_to_f16x8((uint32_t)wq[2 * (j & 1)], (uint32_t)wq[2 * (j & 1) + 1]);
+          p = mfma_f16_k32(__builtin_bit_cast(v8h, cur.q[kk][j]), wb, p);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[cb][r] += p[r] * sw[cb][kk];
@@ -987,7 +978,7 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
           const int row = m0 + (2 * mt + wm) * 16 + 4 * kg + r;
           if (row < cnt) {
             const int col = nt * Q1_BNP + wn * 32 + n2 * 16 + fr;
-            c_act[(size_t)(seg + row) * I + col] = f32_to_bf16_rne(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
+            c_act[(size_t)(seg + row) * I + col] = c_encode(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
           }
         }
   }
@@ -995,21 +986,21 @@ __global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
 
 // ---------------------------------------------------------------------------
 // GEMM2 (+ routing weight), prefill shape: 128 rows x 256 output columns per
-// item on the bf16 MFMA v_mfma_f32_32x32x16_bf16 (full bf16 rate; the 16x16x32
+// item on the fp16 MFMA v_mfma_f32_32x32x16_f16 (full fp16 rate; the 16x16x32
 // form runs at well under half of it), 8 compute waves as 2 (rows) x 4
 // (columns), each 64 x 64 = 2 x 2 tiles of 32 x 32 (row blocks 2 i + wm, so
 // the two row halves interleave), and 4 loader waves.
 //
 // One stage is one 128-wide K block (the W2 scale block): the activation tile
-// (128 rows x 256 B bf16) and the W2 tile (256 rows x 128 B e4m3), 64 KB, in a
+// (128 rows x 256 B fp16) and the W2 tile (256 rows x 128 B e4m3), 64 KB, in a
 // 2-slot LDS ring; the next block's direct loads fly while this one computes.
 // Every load instruction moves 8 whole 128 B row lines, and the LDS holds
 // 32-row x 128 B regions with the 16 B chunks XOR-swizzled per row (sw32), so
 // the fragment reads are conflict-free. K order inside a block (any bijection
 // shared by both operands leaves the MFMA sums unchanged): MFMA step t, lane
 // group g takes K 16 (2 (t / 2) + g) + 8 (t % 2) + [0, 8). A lane therefore
-// reads one 16 B W2 chunk per pair of steps and widens it exactly to bf16,
-// and reads the matching 16 B of bf16 activations per step. The fp32 weight
+// reads one 16 B W2 chunk per pair of steps and widens it exactly to fp16,
+// and reads the matching 16 B of fp16 activations per step. The fp32 weight
 // block scale is applied once per block.
 // ---------------------------------------------------------------------------
 constexpr int Q2_BM = 128;
@@ -1081,26 +1072,26 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
         for (int j = 0; j < 2; ++j) pacc[i][j] = v16f{};
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
-        v8bf bf[2][2];
+        v8h bf[2][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const v4i raw = *reinterpret_cast<const v4i*>(sb + j * Q2_REG + boff[pp]);
-          bf[j][0] = fp8x8_to_bf16x8((uint32_t)raw[0], (uint32_t)raw[1]);
-          bf[j][1] = fp8x8_to_bf16x8((uint32_t)raw[2], (uint32_t)raw[3]);
+          bf[j][0] = fp8x8_to_f16x8((uint32_t)raw[0], (uint32_t)raw[1]);
+          bf[j][1] = fp8x8_to_f16x8((uint32_t)raw[2], (uint32_t)raw[3]);
         }
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-          v8bf af[NI];
+          v8h af[NI];
 #pragma unroll
           for (int i = 0; i < NI; ++i)  // row block 2 i + wm: two 128 B halves of the K block
-            af[i] = *reinterpret_cast<const v8bf*>(st + ((2 * i + wm) * 2 + (pp >> 1)) * Q2_REG + aoff[pp & 1][tt]);
+            af[i] = *reinterpret_cast<const v8h*>(st + ((2 * i + wm) * 2 + (pp >> 1)) * Q2_REG + aoff[pp & 1][tt]);
 #pragma unroll
           for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_bf16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
+            for (int j = 0; j < 2; ++j) pacc[i][j] = mfma_f16_32x32x16(af[i], bf[j][tt], pacc[i][j]);
         }
       }
-      const float sc = *reinterpret_cast<const float*>(st + W2_WSCALE_OFF + 4 * (wn >> 1));
+      const float sc = *reinterpret_cast<const float*>(st + W2_WSCALE_OFF + 4 * (wn >> 1)) * C_LOAD_SCALE;
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll

@@ -1,5 +1,5 @@
 // Tile helpers shared by the LDS-staged kernels: the XCD-aware workgroup
-// order, direct global -> LDS loads, the 32-row swizzle, the 32x32 bf16 MFMA.
+// order, direct global -> LDS loads, the 32-row swizzle, the 32x32 bf16 / fp16 MFMAs.
 #pragma once
 
 #include "moe_common.h"
@@ -30,6 +30,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 __device__ __forceinline__ v16f mfma_bf16_32x32x16(const v8bf& a, const v8bf& b, const v16f& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// The same with fp16 operands.
+__device__ __forceinline__ v16f mfma_f16_32x32x16(const v8h& a, const v8h& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // Offset of row r (0..31), 16 B chunk c (0..7) in a 32-row x 128 B region

@@ -51,6 +51,7 @@ class Workload:
     seed: int
     skew: bool = False
     routed_scaling_factor: float = 2.5
+    official_bias: bool = False  # the official workloads' two-valued bias instead of N(0, 0.1)
 
 
 # Activation seeds. T=1 and T=2 use the first seed (counting up from 1100 and
@@ -72,6 +73,13 @@ WORKLOADS = {
         Workload("prefill_t1024", 1024, 0, 2000),
         Workload("prefill_t8192", 8192, 0, 3000),
         Workload("skew_t4096", 4096, 64, 4002, skew=True),
+        # The two largest official workloads' token counts and offsets
+        # (input_analysis/input_check.ipynb cell 7), with their recorded bias profile
+        # (every bias 4.9375 or 4.96875, cell 5). The seeds are those the trace
+        # replay derives from the uuids "mi355x-trace-11948-128-0" and
+        # "mi355x-trace-14107-32-0", so both paths see the same inputs.
+        Workload("trace_t11948", 11948, 128, 1604742025, official_bias=True),
+        Workload("trace_t14107", 14107, 32, 3697728842, official_bias=True),
     ]
 }
 DECODE_SWEEP = ["decode_t1", "decode_t2", "decode_t4", "decode_t8", "decode_t32", "decode_t64"]
@@ -162,7 +170,15 @@ def gate_weight_bf16(seed: int = GATE_SEED):
     return _normal((seed, 20), (E_GLOBAL, H), float(H) ** -0.5).to(torch.bfloat16)
 
 
-def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool = False):
+def official_bias(seed: int) -> torch.Tensor:
+    """bf16 [256], every value 4.9375 or 4.96875 (two adjacent bf16 values), as in the
+    official workloads (input_analysis/input_check.ipynb cell 5)."""
+    bits = np.random.Generator(np.random.PCG64([seed, 13])).integers(0, 2, E_GLOBAL)
+    return torch.from_numpy(np.float32(4.9375) + np.float32(0.03125) * bits.astype(np.float32)).to(torch.bfloat16)
+
+
+def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool = False,
+                     official: bool = False):
     """(routing_logits fp32 [T,256], routing_bias bf16 [256], hidden e4m3 [T,H], hidden_scale [56,T])."""
     logits = _normal((seed, 10), (T, E_GLOBAL), 1.0)
     if skew:
@@ -170,17 +186,22 @@ def make_activations(T: int, seed: int, local_expert_offset: int = 0, skew: bool
         for g in sorted({int(c) // 32 for c in chosen}):
             logits[:, g * 32:(g + 1) * 32] += 2.0
         logits[:, chosen] += 2.0
-    bias = _normal((seed, 11), (E_GLOBAL,), 0.1).to(torch.bfloat16)
+    bias = official_bias(seed) if official else _normal((seed, 11), (E_GLOBAL,), 0.1).to(torch.bfloat16)
     x = hidden_bf16(T, seed).to(torch.float32)
     hidden, hidden_scale = quantize_1x128(x) if T > 0 else (
         torch.empty((0, H), dtype=torch.float8_e4m3fn), torch.empty((NB_H, 0), dtype=torch.float32))
     return logits, bias, hidden, hidden_scale
 
 
+def workload_activations(w: Workload):
+    """A workload's four activation inputs (make_activations with its parameters)."""
+    return make_activations(w.T, w.seed, w.local_expert_offset, w.skew, w.official_bias)
+
+
 def make_inputs(name_or_workload, device="cpu"):
     """All ten operator inputs, in the reference's positional order, as a list."""
     w = WORKLOADS[name_or_workload] if isinstance(name_or_workload, str) else name_or_workload
-    logits, bias, hidden, hidden_scale = make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    logits, bias, hidden, hidden_scale = workload_activations(w)
     w13, s13, w2, s2 = make_weights()
     args = [logits, bias, hidden, hidden_scale, w13, s13, w2, s2]
     if device != "cpu":

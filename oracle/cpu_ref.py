@@ -80,16 +80,28 @@ def dequant_weight(w, s):
     return wf * sf
 
 
-def route(routing_logits, routing_bias, routed_scaling_factor):
+def route(routing_logits, routing_bias, routed_scaling_factor, exp="torch"):
     """noaux_tc routing, ``ref_moe.py:94-126``.
 
     Returns (topk_idx [T,8] int64 in torch.topk's own order, weights [T,256] fp32,
     s [T,256], s_with_bias [T,256], group_scores [T,8]).
+
+    ``exp="torch"`` evaluates exp(-x) with torch's float32 exp, as the reference
+    does; ``exp="correctly_rounded"`` takes exp(-x) in float64 rounded once to
+    float32 (the HIP kernel's rule). The two differ in the last bit on about
+    0.4 % of logits, which can flip a selection only where two candidates lie
+    within an ulp of each other at a cut; every other step is the reference's.
     """
     T = routing_logits.shape[0]
     logits = routing_logits.to(torch.float32)
     bias = routing_bias.to(torch.float32).reshape(-1)
-    s = 1.0 / (1.0 + torch.exp(-logits))
+    if exp == "torch":
+        e = torch.exp(-logits)
+    elif exp == "correctly_rounded":
+        e = torch.exp(-logits.to(torch.float64)).to(torch.float32)
+    else:
+        raise ValueError(exp)
+    s = 1.0 / (1.0 + e)
     s_with_bias = s + bias
     grouped = s_with_bias.view(T, N_GROUP, GROUP_SIZE)
     top2_vals, _ = torch.topk(grouped, k=2, dim=2, largest=True, sorted=False)
@@ -143,13 +155,13 @@ def expert_ffn(A_e, W13_e, W2_e):
 @torch.no_grad()
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale,
         gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
-        local_expert_offset, routed_scaling_factor, materialize_all=False):
+        local_expert_offset, routed_scaling_factor, materialize_all=False, exp="torch"):
     """Whole operator on the CPU, ``ref_moe.py:4-168``; returns bf16 [T, 7168].
 
     ``materialize_all=True`` dequantises all 32 experts up front as the reference
     does (its dominant fixed cost, used for the CPU baseline timing). The default
     dequantises each expert when it is first used; the values are elementwise
-    identical, so the output is the same.
+    identical, so the output is the same. ``exp`` as in ``route``.
     """
     T = check_geometry(routing_logits, hidden_states, hidden_states_scale, gemm1_weights,
                        gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, routing_bias)
@@ -157,7 +169,7 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale,
     if materialize_all:
         W13_all = dequant_weight(gemm1_weights, gemm1_weights_scale)
         W2_all = dequant_weight(gemm2_weights, gemm2_weights_scale)
-    topk_idx, weights, _, _, _ = route(routing_logits, routing_bias, routed_scaling_factor)
+    topk_idx, weights, _, _, _ = route(routing_logits, routing_bias, routed_scaling_factor, exp=exp)
 
     output = torch.zeros((T, H), dtype=torch.float32)
     lists = dispatch(topk_idx, local_expert_offset)

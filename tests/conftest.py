@@ -102,10 +102,7 @@ def trace_case_tensors(uuid, T):
     """Recorded inputs of a trace case: fp32 N(0,1) logits and the two-level bf16 bias."""
     from flashinfer_mlsys_amd import trace, workloads as wl
     seed = trace.TraceWorkload(uuid, T, {}).seed
-    logits = wl._normal((seed, 10), (T, 256), 1.0)
-    bits = np.random.Generator(np.random.PCG64([seed, 13])).integers(0, 2, 256)
-    bias = torch.from_numpy(4.9375 + 0.03125 * bits.astype(np.float32)).to(torch.bfloat16)
-    return logits, bias
+    return wl._normal((seed, 10), (T, 256), 1.0), wl.official_bias(seed)
 
 
 def write_trace_cases(root, cases=TRACE_CASES):

@@ -33,7 +33,7 @@ def test_e4m3_decode_matches_spec():
 def test_inputs_regenerate(name):
     w = wl.WORKLOADS[name]
     g = load_golden(name)
-    acts = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    acts = wl.workload_activations(w)
     assert [wl.fingerprint(a) for a in acts] == [str(h) for h in g["in_sha256"]]
 
 
@@ -49,7 +49,7 @@ def test_weights_regenerate():
 def test_oracle_routing_matches_reference(name):
     w = wl.WORKLOADS[name]
     g = load_golden(name)
-    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    lg, b, _, _ = wl.workload_activations(w)
     topk_idx = cpu_ref.route(lg, b, w.routed_scaling_factor)[0]
     np.testing.assert_array_equal(cpu_ref.sorted_selection(topk_idx).numpy(), g["sel_ids"].astype(np.int64))
     lists = cpu_ref.dispatch(topk_idx, w.local_expert_offset)
@@ -58,11 +58,27 @@ def test_oracle_routing_matches_reference(name):
         np.testing.assert_array_equal(a.numpy(), b_)
 
 
+@pytest.mark.parametrize("name", ALL)
+def test_oracle_correctly_rounded_exp_routing(name):
+    """exp="correctly_rounded" (exp(-x) in float64, rounded once: the kernel's rule)
+    keeps every reference selection of the workloads, and its sigmoid equals an
+    independent numpy evaluation bit for bit."""
+    w = wl.WORKLOADS[name]
+    g = load_golden(name)
+    lg, b, _, _ = wl.workload_activations(w)
+    topk_idx, _, s, _, _ = cpu_ref.route(lg, b, w.routed_scaling_factor, exp="correctly_rounded")
+    np.testing.assert_array_equal(cpu_ref.sorted_selection(topk_idx).numpy(), g["sel_ids"].astype(np.int64))
+    one = np.float32(1.0)
+    x = lg[:64].numpy()
+    s_np = one / (one + np.exp(-x.astype(np.float64)).astype(np.float32))
+    np.testing.assert_array_equal(s[:64].numpy(), s_np)
+
+
 @pytest.mark.parametrize("name", ["t16", "skew_t4096", "prefill_t1024"])
 def test_routing_brute_force(name):
     """Exhaustive group-subset search (70 subsets) + full sort on the first 24 tokens."""
     w = wl.WORKLOADS[name]
-    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    lg, b, _, _ = wl.workload_activations(w)
     lg = lg[:24]
     ids, wts = np_ref.brute_force_route(lg.numpy(), b.float().numpy(), w.routed_scaling_factor)
     topk_idx, dense, _, _, _ = cpu_ref.route(lg, b, w.routed_scaling_factor)
@@ -75,7 +91,7 @@ def test_routing_brute_force(name):
 
 def test_routing_invariants_t8192():
     w = wl.WORKLOADS["prefill_t8192"]
-    lg, b, _, _ = wl.make_activations(w.T, w.seed, w.local_expert_offset, w.skew)
+    lg, b, _, _ = wl.workload_activations(w)
     topk_idx, dense, s, sb, gs = cpu_ref.route(lg, b, w.routed_scaling_factor)
     sel = cpu_ref.sorted_selection(topk_idx)
     assert (sel[:, 1:] > sel[:, :-1]).all()
@@ -182,8 +198,8 @@ def _transposed_block_scale(w, s):
     return wf * sf
 
 
-def _route_without_bias(logits, bias, rsf):
-    return _orig_route(logits, torch.zeros_like(bias), rsf)
+def _route_without_bias(logits, bias, rsf, exp="torch"):
+    return _orig_route(logits, torch.zeros_like(bias), rsf, exp=exp)
 
 
 _orig_route = cpu_ref.route
