@@ -65,6 +65,11 @@ def _contig(t):
     return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
 
 
+def _header_words(T: int) -> int:
+    """MOE_FP8_DISPATCH_HEADER_WORDS(T): the header, then 32 counts per 256-token chunk."""
+    return _lib.MOE_FP8_HEADER_WORDS + 32 * ((T + 255) // 256)
+
+
 def workspace_size(T: int) -> int:
     """Device workspace bytes ``kernel`` needs for T tokens."""
     return int(_lib.load().moe_fp8_workspace_size(int(T)))
@@ -308,7 +313,7 @@ def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
     _on_gpu(topk_ids, "topk_ids")
     T = topk_ids.shape[0]
     dev = topk_ids.device
-    header = torch.zeros(128, dtype=torch.int32, device=dev)
+    header = torch.zeros(_header_words(T), dtype=torch.int32, device=dev)
     perm_tok = torch.full((max(1, TOP_K * T),), -1, dtype=torch.int32, device=dev)
     perm_w = torch.zeros((max(1, TOP_K * T),), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
@@ -317,7 +322,7 @@ def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
                                             header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
                                             tok_pair.data_ptr() if T else header.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_dispatch")
-    return header, perm_tok, perm_w, tok_pair
+    return header[:_lib.MOE_FP8_HEADER_WORDS], perm_tok, perm_w, tok_pair
 
 
 @torch.no_grad()
@@ -335,12 +340,12 @@ def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_sca
     dev = routing_logits.device
     ids = torch.empty((T, TOP_K), dtype=torch.int32, device=dev)
     w = torch.empty((T, TOP_K), dtype=torch.float32, device=dev)
-    header = torch.zeros(128, dtype=torch.int32, device=dev)
+    header = torch.zeros(_header_words(T), dtype=torch.int32, device=dev)
     perm_tok = torch.full((max(1, TOP_K * T),), -1, dtype=torch.int32, device=dev)
     perm_w = torch.zeros((max(1, TOP_K * T),), dtype=torch.float32, device=dev)
     pair = torch.full((T, TOP_K), -7, dtype=torch.int32, device=dev)
     if T == 0:
-        return ids, w, header, perm_tok, perm_w, pair
+        return ids, w, header[:_lib.MOE_FP8_HEADER_WORDS], perm_tok, perm_w, pair
     lg, b = _contig(routing_logits), _contig(routing_bias.reshape(-1))
     with torch.cuda.device(dev):
         code = _lib.load().moe_fp8_route_dispatch(int(shape), lg.data_ptr(), b.data_ptr(), T, int(local_expert_offset),
@@ -348,4 +353,4 @@ def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_sca
                                                   header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
                                                   pair.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_route_dispatch")
-    return ids, w, header, perm_tok, perm_w, pair
+    return ids, w, header[:_lib.MOE_FP8_HEADER_WORDS], perm_tok, perm_w, pair

@@ -20,6 +20,8 @@ MOE_ERR_HIP = -5
 MOE_ERR_ARG = -6
 MOE_ERR_NOALLOC_SIZE = -7
 MOE_FP8_NOALLOC_MAX_TOKENS = 64
+MOE_FP8_MAX_TOKENS = 1 << 17
+MOE_FP8_HEADER_WORDS = 128
 
 MOE_SHAPE_AUTO = 0
 MOE_SHAPE_PREFILL = 1

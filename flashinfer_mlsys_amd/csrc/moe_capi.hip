@@ -13,7 +13,7 @@
 namespace moe {
 hipError_t launch_route(const float*, const uint16_t*, int, float, int32_t*, float*, int32_t*, hipStream_t);
 hipError_t launch_dispatch(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
-                           hipStream_t);
+                           int32_t*, hipStream_t);
 hipError_t launch_dispatch_small(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
                                  hipStream_t);
 hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const uint8_t*, const float*, int, int,
@@ -89,7 +89,7 @@ struct Call {
   bool decode;  // T <= 64 and the shape is not forced to the prefill kernels
   hipStream_t stream;
   moe::DispatchHeader* hdr;
-  int32_t *topk_ids, *tok_pair, *perm_tok;
+  int32_t *topk_ids, *tok_pair, *perm_tok, *chunk_counts;
   float *topk_w, *perm_w, *partial;
   uint16_t* c_act;
 };
@@ -136,6 +136,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   c.perm_w = reinterpret_cast<float*>(ws + L.perm_w);
   c.c_act = reinterpret_cast<uint16_t*>(ws + L.c_act);
   c.partial = reinterpret_cast<float*>(ws + L.partial);
+  c.chunk_counts = reinterpret_cast<int32_t*>(ws + L.chunk_counts);
   return 1;  // valid, work to do
 }
 
@@ -156,7 +157,7 @@ hipError_t run_stage(int stage, const Call& c) {
         hipError_t e = launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, c.tok_pair, c.stream);
         if (e != hipSuccess) return e;
         return launch_dispatch(c.topk_ids, c.topk_w, c.T, c.offset, c.hdr, c.perm_tok, c.perm_w, c.tok_pair,
-                               c.stream);
+                               c.chunk_counts, c.stream);
       }
     case 1:
       if (c.decode) {
@@ -261,7 +262,7 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
     return MOE_ERR_ALIGN;
   hipError_t e = moe::launch_dispatch(topk_ids, topk_w, (int)T, clamp_offset(local_expert_offset),
                                       reinterpret_cast<moe::DispatchHeader*>(header), perm_tok, perm_w, tok_pair,
-                                      reinterpret_cast<hipStream_t>(stream));
+                                      header + MOE_FP8_HEADER_WORDS, reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
@@ -287,7 +288,8 @@ int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_
   e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, decode ? nullptr : tok_pair, s);
   if (e == hipSuccess) {
     e = decode ? launch_dispatch_small(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)
-               : launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s);
+               : launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, header + MOE_FP8_HEADER_WORDS,
+                                 s);
   }
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }

@@ -106,12 +106,18 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 
 __host__ __device__ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Dispatch (prefill shape) works on chunks of this many tokens and exchanges
+// 32 counts per chunk between its two kernels.
+constexpr int DISPATCH_CHUNK = 256;
+__host__ __device__ constexpr int dispatch_chunks(int64_t T) { return (int)((T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK); }
+
 // Workspace layout for T tokens (worst case P = 8T routed pairs). The fp32
-// partial rows come last: only the prefill kernels use them, so a decode-shape
-// call needs `total` bytes of make(T, false) (the same offsets, no partial rows).
+// partial rows and the dispatch's chunk counts come last: only the prefill
+// kernels use them, so a decode-shape call needs `total` bytes of make(T, false)
+// (the same offsets, without those regions).
 struct WorkspaceLayout {
   size_t hdr = 0, topk_ids = 0, topk_w = 0, tok_pair = 0, perm_tok = 0, perm_w = 0, c_act = 0, partial = 0,
-         total = 0;
+         chunk_counts = 0, total = 0;
   __host__ __device__ static constexpr WorkspaceLayout make(int64_t T, bool with_partial = true) {
     WorkspaceLayout L;
     const size_t P = (size_t)T * TOP_K;
@@ -124,6 +130,7 @@ struct WorkspaceLayout {
     L.perm_w = o;   o += align_up(P * 4, 256);
     L.c_act = o;    o += align_up(P * I * 2, 256);
     L.partial = o;  o += with_partial ? align_up(P * H * 4, 256) : 0;
+    L.chunk_counts = o; o += with_partial ? align_up((size_t)dispatch_chunks(T) * E_LOCAL * 4, 256) : 0;
     L.total = o;
     return L;
   }

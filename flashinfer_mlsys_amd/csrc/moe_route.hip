@@ -7,12 +7,11 @@
 //                     top-8 by 8 rounds of wave arg-max, and the reference's
 //                     nth_element order where equal keys straddle a cut
 //                     (moe_route_token.h, moe_route_ties.h).
-// dispatch_kernel  -- reference moe/ref_moe.py:131-145 (for each local expert the
-//                     ascending list of tokens that selected it). One workgroup
-//                     per local expert: a histogram of all local ids gives every
-//                     segment's start, then a ballot/popcount scan writes the
-//                     expert's tokens in ascending order. No atomics on global
-//                     memory, no host synchronisation.
+// dispatch_count_kernel, dispatch_scatter_kernel -- reference
+//                     moe/ref_moe.py:131-145 (for each local expert the ascending
+//                     list of tokens that selected it): per-chunk counts, then
+//                     segment starts and ballot/popcount ranks. No atomics, no
+//                     host synchronisation.
 // dispatch_small_kernel -- the decode-size dispatch (T <= 64) in one workgroup.
 #include "moe_common.h"
 #include "moe_route_token.h"
@@ -29,85 +28,6 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   if (t >= T) return;
   route_token(logits, bias, t, rsf, topk_ids, topk_w, tok_pair, &tie[threadIdx.x >> 6]);
 }
-
-// One workgroup per local expert (grid = 32): each walks all T tokens in
-// 256-token steps (two barriers per step), so its time grows with T; used
-// above DISPATCH_CHUNKED_MAX_T tokens, where dispatch_chunked_kernel's total
-// work (which grows with T^2) would be larger.
-__global__ __launch_bounds__(256) void dispatch_kernel(const int32_t* __restrict__ topk_ids,
-                                                       const float* __restrict__ topk_w, int T, int offset,
-                                                       DispatchHeader* __restrict__ hdr,
-                                                       int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,
-                                                       int32_t* __restrict__ tok_pair) {
-  __shared__ int hist[E_LOCAL];
-  __shared__ int wave_cnt[4];
-  __shared__ int seg_base;
-  const int le = blockIdx.x;
-  const int ge = offset + le;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < E_LOCAL) hist[tid] = 0;
-  __syncthreads();
-  for (int t = tid; t < T; t += 256) {
-    const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
-    const int4 a = row[0], b = row[1];
-    const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int j = 0; j < TOP_K; ++j) {
-      const unsigned l = (unsigned)(v[j] - offset);
-      if (l < (unsigned)E_LOCAL) atomicAdd(&hist[l], 1);
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0, nact = 0;
-    for (int e = 0; e < E_LOCAL; ++e) {
-      if (e == le) seg_base = acc;
-      if (le == 0) {
-        hdr->counts[e] = hist[e];
-        hdr->seg_start[e] = acc;
-        if (hist[e] > 0) hdr->active[nact++] = e;
-      }
-      acc += hist[e];
-    }
-    if (le == 0) {
-      hdr->seg_start[E_LOCAL] = acc;
-      hdr->n_active = nact;
-      for (int e = nact; e < E_LOCAL; ++e) hdr->active[e] = -1;
-    }
-  }
-  __syncthreads();
-  int base = seg_base;
-  const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int t0 = 0; t0 < T; t0 += 256) {
-    const int t = t0 + tid;
-    int slot = -1;
-    if (t < T) {
-      const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
-      const int4 a = row[0], b = row[1];
-      const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int j = 0; j < TOP_K; ++j) slot = v[j] == ge ? j : slot;
-    }
-    const unsigned long long m = __ballot(slot >= 0);
-    if (lane == 0) wave_cnt[wave] = __popcll(m);
-    __syncthreads();
-    int wbase = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      wbase += w < wave ? wave_cnt[w] : 0;
-      total += wave_cnt[w];
-    }
-    if (slot >= 0) {
-      const int pos = base + wbase + __popcll(m & lt_mask);
-      perm_tok[pos] = t;
-      perm_w[pos] = topk_w[(size_t)t * TOP_K + slot];
-      tok_pair[(size_t)t * TOP_K + slot] = pos;
-    }
-    base += total;
-    __syncthreads();
-  }
-}
-
 
 // Dispatch of up to 64 tokens in one workgroup with the same device code the
 // decode GEMM1 kernel runs in each of its workgroups (dispatch tap).
@@ -146,65 +66,27 @@ hipError_t launch_dispatch_small(const int32_t* topk_ids, const float* topk_w, i
   return hipGetLastError();
 }
 
-// One workgroup per 512-token chunk (grid = ceil(T / 512)), all chunks in
-// parallel and with no scratch memory: every workgroup histograms the local
-// ids of all T tokens (totals -> segment starts) and of the tokens before its
-// chunk (its offset inside each segment), then ranks its own tokens per expert
-// with one wave ballot per expert and a prefix over its 8 waves. Within each
-// expert the tokens stay in ascending order (reference ref_moe.py:131-145).
-// Workgroup 0 writes the header.
-constexpr int DISPATCH_CHUNK = 512;
-constexpr int DISPATCH_CHUNKED_MAX_T = 131072;
+// Dispatch in two kernels over chunks of DISPATCH_CHUNK tokens, with the
+// per-chunk counts in between (no atomics, no host synchronisation):
+//  * dispatch_count_kernel: workgroup c counts, per local expert, the tokens of
+//    chunk c that selected it (one ballot per expert and wave) into
+//    chunk_counts[c][32];
+//  * dispatch_scatter_kernel: workgroup c sums the chunk counts of all chunks
+//    (totals -> segment starts) and of the chunks before it (its offset inside
+//    each segment), then ranks its own tokens per expert with one ballot per
+//    expert and wave and a prefix over its waves. Within each expert the tokens
+//    stay in ascending order (reference ref_moe.py:131-145). Workgroup 0 writes
+//    the header.
+// Each workgroup reads its chunk's ids and 32 ints per chunk, so the work grows
+// linearly with T (a single kernel in which every workgroup re-counts all T
+// tokens grows with T^2).
+constexpr int DISPATCH_WAVES = DISPATCH_CHUNK / 64;
 
-__global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
-    const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
-    DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,
-    int32_t* __restrict__ tok_pair) {
-  constexpr int NW = DISPATCH_CHUNK / 64;
-  __shared__ int hist_all[E_LOCAL], hist_pre[E_LOCAL], seg[E_LOCAL];
-  __shared__ unsigned long long wmask[NW][E_LOCAL];  // per wave and expert: lanes whose token selected it
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t0 = blockIdx.x * DISPATCH_CHUNK;
-  if (tid < E_LOCAL) {
-    hist_all[tid] = 0;
-    hist_pre[tid] = 0;
-  }
-  __syncthreads();
-  for (int t = tid; t < T; t += DISPATCH_CHUNK) {
-    const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
-    const int4 a = row[0], b = row[1];
-    const int v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int j = 0; j < TOP_K; ++j) {
-      const unsigned l = (unsigned)(v[j] - offset);
-      if (l < (unsigned)E_LOCAL) {
-        atomicAdd(&hist_all[l], 1);
-        if (t < t0) atomicAdd(&hist_pre[l], 1);
-      }
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0, nact = 0;
-    for (int e = 0; e < E_LOCAL; ++e) {
-      seg[e] = acc;
-      if (blockIdx.x == 0) {
-        hdr->counts[e] = hist_all[e];
-        hdr->seg_start[e] = acc;
-        if (hist_all[e] > 0) hdr->active[nact++] = e;
-      }
-      acc += hist_all[e];
-    }
-    if (blockIdx.x == 0) {
-      hdr->seg_start[E_LOCAL] = acc;
-      hdr->n_active = nact;
-      for (int e = nact; e < E_LOCAL; ++e) hdr->active[e] = -1;
-    }
-  }
-  // this chunk's tokens: which local experts each selected, and in which slot
-  const int t = t0 + tid;
+__device__ __forceinline__ uint32_t local_mask(const int32_t* __restrict__ topk_ids, int t, int T, int offset,
+                                               int (&slot_of)[TOP_K]) {
   uint32_t mask = 0u;
-  int slot_of[TOP_K];
+#pragma unroll
+  for (int j = 0; j < TOP_K; ++j) slot_of[j] = -1;
   if (t < T) {
     const int4* row = reinterpret_cast<const int4*>(topk_ids + (size_t)t * TOP_K);
     const int4 a = row[0], b = row[1];
@@ -215,6 +97,84 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
       if ((unsigned)slot_of[j] < (unsigned)E_LOCAL) mask |= 1u << slot_of[j];
     }
   }
+  return mask;
+}
+
+__global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T,
+                                                                        int offset,
+                                                                        int32_t* __restrict__ chunk_counts) {
+  __shared__ int wcnt[DISPATCH_WAVES][E_LOCAL];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int slot_of[TOP_K];
+  const uint32_t mask = local_mask(topk_ids, blockIdx.x * DISPATCH_CHUNK + tid, T, offset, slot_of);
+  int mine = 0;  // lane e < 32: this wave's tokens that selected expert e
+#pragma unroll
+  for (int e = 0; e < E_LOCAL; ++e) {
+    const int c = __popcll(__ballot((mask >> e) & 1u));
+    mine = lane == e ? c : mine;
+  }
+  if (lane < E_LOCAL) wcnt[wave][lane] = mine;
+  __syncthreads();
+  if (tid < E_LOCAL) {
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < DISPATCH_WAVES; ++w) s += wcnt[w][tid];
+    chunk_counts[(size_t)blockIdx.x * E_LOCAL + tid] = s;
+  }
+}
+
+__global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_scatter_kernel(
+    const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int offset,
+    const int32_t* __restrict__ chunk_counts, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
+    float* __restrict__ perm_w, int32_t* __restrict__ tok_pair) {
+  constexpr int PARTS = DISPATCH_CHUNK / E_LOCAL;  // threads per expert summing the chunk counts
+  __shared__ int part_all[PARTS][E_LOCAL], part_pre[PARTS][E_LOCAL];
+  __shared__ int seg[E_LOCAL], pre[E_LOCAL];
+  __shared__ unsigned long long wmask[DISPATCH_WAVES][E_LOCAL];  // per wave and expert: lanes whose token selected it
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nchunks = gridDim.x, chunk = blockIdx.x;
+  {
+    const int e = tid & (E_LOCAL - 1), part = tid / E_LOCAL;
+    int all = 0, before = 0;
+    for (int c = part; c < nchunks; c += PARTS) {
+      const int v = chunk_counts[(size_t)c * E_LOCAL + e];
+      all += v;
+      before += c < chunk ? v : 0;
+    }
+    part_all[part][e] = all;
+    part_pre[part][e] = before;
+  }
+  __syncthreads();
+  if (tid < E_LOCAL) {  // lanes 0-31 of wave 0: one expert each
+    int total = 0, b = 0;
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) {
+      total += part_all[p][tid];
+      b += part_pre[p][tid];
+    }
+    int incl = total;  // inclusive scan over the experts
+#pragma unroll
+    for (int d = 1; d < E_LOCAL; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      if (tid >= d) incl += o;
+    }
+    seg[tid] = incl - total;
+    pre[tid] = b;
+    if (chunk == 0) {
+      const unsigned long long act = __ballot(total > 0);
+      hdr->counts[tid] = total;
+      hdr->seg_start[tid] = incl - total;
+      if (tid == E_LOCAL - 1) hdr->seg_start[E_LOCAL] = incl;
+      const int nact = __popcll(act);
+      if (tid == 0) hdr->n_active = nact;
+      if (total > 0) hdr->active[__popcll(act & ((1ull << tid) - 1ull))] = tid;
+      if (tid >= nact) hdr->active[tid] = -1;
+    }
+  }
+  // this chunk's tokens: which local experts each selected, and in which slot
+  const int t = chunk * DISPATCH_CHUNK + tid;
+  int slot_of[TOP_K];
+  const uint32_t mask = local_mask(topk_ids, t, T, offset, slot_of);
   for (int e = 0; e < E_LOCAL; ++e) {  // uniform over the wave
     const unsigned long long m = __ballot((mask >> e) & 1u);
     if (lane == 0) wmask[wave][e] = m;
@@ -228,7 +188,7 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
       if ((unsigned)e >= (unsigned)E_LOCAL) continue;
       int before = 0;  // earlier waves' tokens of this chunk that selected e
       for (int w = 0; w < wave; ++w) before += __popcll(wmask[w][e]);
-      const int pos = seg[e] + hist_pre[e] + before + __popcll(wmask[wave][e] & lt);
+      const int pos = seg[e] + pre[e] + before + __popcll(wmask[wave][e] & lt);
       perm_tok[pos] = t;
       perm_w[pos] = topk_w[(size_t)t * TOP_K + j];
       tok_pair[(size_t)t * TOP_K + j] = pos;
@@ -237,15 +197,15 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_chunked_kernel(
 }
 
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int offset, DispatchHeader* hdr,
-                           int32_t* perm_tok, float* perm_w, int32_t* tok_pair, hipStream_t stream) {
-  if (T <= DISPATCH_CHUNKED_MAX_T) {
-    const int chunks = T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1;
-    hipLaunchKernelGGL(dispatch_chunked_kernel, dim3(chunks), dim3(DISPATCH_CHUNK), 0, stream, topk_ids, topk_w, T,
-                       offset, hdr, perm_tok, perm_w, tok_pair);
-  } else {
-    hipLaunchKernelGGL(dispatch_kernel, dim3(E_LOCAL), dim3(256), 0, stream, topk_ids, topk_w, T, offset, hdr,
-                       perm_tok, perm_w, tok_pair);
-  }
+                           int32_t* perm_tok, float* perm_w, int32_t* tok_pair, int32_t* chunk_counts,
+                           hipStream_t stream) {
+  const int chunks = T > 0 ? dispatch_chunks(T) : 1;
+  hipLaunchKernelGGL(dispatch_count_kernel, dim3(chunks), dim3(DISPATCH_CHUNK), 0, stream, topk_ids, T, offset,
+                     chunk_counts);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(chunks), dim3(DISPATCH_CHUNK), 0, stream, topk_ids, topk_w, T,
+                     offset, chunk_counts, hdr, perm_tok, perm_w, tok_pair);
   return hipGetLastError();
 }
 

@@ -148,7 +148,7 @@ __device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, 
   dispatch_small_lists(T, offset, d);
 }
 
-// Writes the dispatch to memory in the layout of dispatch_kernel (header,
+// Writes the dispatch to memory in the layout of the dispatch kernels (header,
 // perm_tok, perm_w, tok_pair). Called by every thread of one workgroup.
 __device__ __forceinline__ void store_small_dispatch(const SmallDispatch& d, int T, DispatchHeader* __restrict__ hdr,
                                                      int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,

@@ -37,7 +37,15 @@ enum {
  * T <= 64 and the prefill kernels above (AUTO), or the prefill kernels at any T. */
 enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
-#define MOE_FP8_MAX_TOKENS (1 << 20)
+/* Largest T any entry point accepts: the worst-case workspace (8 local pairs per
+ * token, moe_fp8_workspace_size) is about 262 KB per token, 34 GB at this T. */
+#define MOE_FP8_MAX_TOKENS (1 << 17)
+
+/* Words of the `header` buffer moe_fp8_dispatch and moe_fp8_route_dispatch take
+ * for T tokens: the dispatch header (MOE_FP8_HEADER_WORDS) followed by 32 counts
+ * per chunk of 256 tokens, which the two dispatch kernels exchange. */
+#define MOE_FP8_HEADER_WORDS 128
+#define MOE_FP8_DISPATCH_HEADER_WORDS(T) (MOE_FP8_HEADER_WORDS + 32 * (((T) + 255) / 256))
 
 /* Bytes of device workspace one forward call needs for T tokens (worst case
  * of 8 routed local pairs per token). */
@@ -139,8 +147,9 @@ int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int
  * Dispatch stage alone (reference moe/ref_moe.py:131-145; the nonzero / sort /
  * cumsum dispatch of solution/cuda/kernel_v2.cu:208-244, without its host sync).
  * From the routing stage's ids and weights, writes
- *   header   int32 [128]: counts[32], seg_start[33] (seg_start[32] = P),
- *            n_active, active[32] (local ids with tokens, ascending), padding
+ *   header   int32 [MOE_FP8_DISPATCH_HEADER_WORDS(T)]: counts[32], seg_start[33]
+ *            (seg_start[32] = P), n_active, active[32] (local ids with tokens,
+ *            ascending), padding to 128 words, then the per-chunk counts
  *   perm_tok int32 [8T]: for each local expert in order, its tokens ascending
  *   perm_w   fp32  [8T]: the routing weight of each (token, expert) pair
  *   tok_pair int32 [T, 8]: pair index of slot j of token t; must hold -1 on
@@ -153,7 +162,7 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
  * Routing and dispatch as moe_fp8_forward_shape(shape, ...) runs them (in the
  * decode shape the routing kernel plus, in one workgroup, the dispatch code
  * every decode GEMM1 workgroup runs; otherwise the two kernels above), writing
- * topk_ids / topk_w [T, 8], header [128], perm_tok / perm_w [8T] and
+ * topk_ids / topk_w [T, 8], header [MOE_FP8_DISPATCH_HEADER_WORDS(T)], perm_tok / perm_w [8T] and
  * tok_pair [T, 8] (fully written: -1 for non-local slots). Parity tap for
  * reference moe/ref_moe.py:94-145.
  */

@@ -45,6 +45,9 @@ def test_abi_version_and_strings(lib):
 
 def test_workspace_size(lib):
     assert lib.moe_fp8_workspace_size(-1) == 0
+    assert lib.moe_fp8_workspace_size(_lib.MOE_FP8_MAX_TOKENS + 1) == 0
+    # the worst case stays allocatable on one 288 GB GPU
+    assert lib.moe_fp8_workspace_size(_lib.MOE_FP8_MAX_TOKENS) < 40e9
     assert lib.moe_fp8_workspace_size(0) > 0
     prev = 0
     for T in (1, 2, 16, 1024, 8192):
@@ -66,7 +69,7 @@ def _fwd(lib, T=1, ptrs=None, ws_bytes=1 << 40):
 
 def test_forward_argument_errors(lib):
     assert _fwd(lib, T=-1) == _lib.MOE_ERR_SIZE
-    assert _fwd(lib, T=(1 << 20) + 1) == _lib.MOE_ERR_SIZE
+    assert _fwd(lib, T=_lib.MOE_FP8_MAX_TOKENS + 1) == _lib.MOE_ERR_SIZE
     assert _fwd(lib, T=0) == _lib.MOE_OK
     ptrs = [FAKE] * 8
     ptrs[3] = None
@@ -86,7 +89,7 @@ def test_noalloc_argument_errors(lib):
     """Rejected on the host before any GPU call: beyond its 64-token limit, T < 0."""
     f = lib.moe_fp8_forward_noalloc
     assert f(*[FAKE] * 8, 65, 0, 2.5, FAKE, None) == _lib.MOE_ERR_NOALLOC_SIZE
-    assert f(*[FAKE] * 8, 1 << 20, 0, 2.5, FAKE, None) == _lib.MOE_ERR_NOALLOC_SIZE
+    assert f(*[FAKE] * 8, _lib.MOE_FP8_MAX_TOKENS, 0, 2.5, FAKE, None) == _lib.MOE_ERR_NOALLOC_SIZE
     assert f(*[FAKE] * 8, -1, 0, 2.5, FAKE, None) == _lib.MOE_ERR_SIZE
     assert f(*[FAKE] * 8, 0, 0, 2.5, FAKE, None) == _lib.MOE_OK
     assert lib.moe_fp8_strerror(_lib.MOE_ERR_NOALLOC_SIZE).startswith(b"token count beyond")
@@ -105,7 +108,7 @@ def test_quantize_argument_errors(lib):
     q = lib.moe_fp8_quantize_activations
     assert q(FAKE, 0, FAKE, FAKE, None) == _lib.MOE_OK
     assert q(FAKE, -1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert q(FAKE, (1 << 20) + 1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert q(FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
     assert q(None, 4, FAKE, FAKE, None) == _lib.MOE_ERR_NULL
     assert q(FAKE, 4, FAKE, None, None) == _lib.MOE_ERR_NULL
     assert q(FAKE, 4, FAKE + 8, FAKE, None) == _lib.MOE_ERR_ALIGN
@@ -115,7 +118,7 @@ def test_router_argument_errors(lib):
     r = lib.moe_fp8_router_logits
     assert r(FAKE, FAKE, 0, None, None) == _lib.MOE_OK  # nothing to do, nothing read
     assert r(FAKE, FAKE, -1, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert r(FAKE, FAKE, (1 << 20) + 1, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, None) == _lib.MOE_ERR_SIZE
     assert r(None, FAKE, 4, FAKE, None) == _lib.MOE_ERR_NULL
     assert r(FAKE, None, 4, FAKE, None) == _lib.MOE_ERR_NULL
     assert r(FAKE, FAKE, 4, None, None) == _lib.MOE_ERR_NULL
@@ -127,7 +130,7 @@ def test_router_quantize_argument_errors(lib):
     r = lib.moe_fp8_router_quantize
     assert r(FAKE, FAKE, 0, None, None, None, None) == _lib.MOE_OK  # nothing to do, nothing read
     assert r(FAKE, FAKE, -1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert r(FAKE, FAKE, (1 << 20) + 1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
     for i in range(5):
         args = [FAKE] * 5
         args[i] = None

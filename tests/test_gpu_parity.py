@@ -148,11 +148,12 @@ def _synthetic_ids(T, offset, seed):
     return ids, w
 
 
-@pytest.mark.parametrize("T,offset", [(20000, 64), (140000, 0)])
+@pytest.mark.parametrize("T,offset", [(20000, 64), (131072, 0), (777, 200)])
 def test_dispatch_large_synthetic(dev, T, offset):
-    """Dispatch bit-exact at sizes past the benchmark's: many 512-token chunks
-    (T=20000) and the per-expert kernel used above 131072 tokens (T=140000),
-    against a numpy restatement of ref_moe.py:131-145."""
+    """Dispatch bit-exact at sizes past the benchmark's: many 256-token chunks
+    (T=20000), the largest token count the library accepts (T=131072: 512
+    chunks) and a ragged last chunk (T=777), against a numpy restatement of
+    ref_moe.py:131-145."""
     _say(f"dispatch synthetic T={T} offset={offset}")
     ids, w = _synthetic_ids(T, offset, seed=T)
     ids_d = torch.from_numpy(ids).to(dev)
