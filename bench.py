@@ -23,7 +23,7 @@ Printed JSON line (rank 0, one line):
   also          the other benchmark configurations (prefill 1024 / 8192, skew 4096, and the two
                 largest official token counts 11,948 / 14,107 with their bias profile), each with
                 a roofline object against its binding roof (HBM bytes / 8 TB/s or e4m3 GEMM1 at
-                5.0 PFLOP/s + bf16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; the drop-in
+                5.0 PFLOP/s + fp16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; the drop-in
                 Python entry point timed at T=1 (host cost included); and the producer-side
                 kernels (FP8 activation quantiser, router GEMM, both fused) at T = 64 and 8192
 """
@@ -49,7 +49,7 @@ from flashinfer_mlsys_amd import workloads as wl  # noqa: E402
 METRIC = "µs/call & tokens/s, FP8 MoE 32 local experts, T=1…8192; % MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0   # dense e4m3 MFMA
-BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA (bf16 the same)
 STAGES = ["route_dispatch", "gemm1", "gemm2", "combine"]
 # the reference harness's timing protocol (scripts/run_local.py:33: BenchmarkConfig)
 HARNESS_WARMUP, HARNESS_ITERS, HARNESS_TRIALS = 3, 100, 5
@@ -232,10 +232,10 @@ def cpu_oracle_us(name):
 
 def binding_roofline(c, us):
     """The configuration's binding roof: HBM (algorithmic bytes at 8 TB/s) or MFMA (GEMM1 on the
-    e4m3 MFMA at 5.0 PFLOP/s plus GEMM2 on the bf16 MFMA at 2.5 PFLOP/s), whichever is slower."""
+    e4m3 MFMA at 5.0 PFLOP/s plus GEMM2 on the fp16 MFMA at 2.5 PFLOP/s), whichever is slower."""
     hbm_us = c.bytes / (HBM_PEAK_GBS * 1e9) * 1e6
     mfma_us = (c.P * GEMM1_FLOPS_PER_PAIR / (FP8_PEAK_TFLOPS * 1e12)
-               + c.P * GEMM2_FLOPS_PER_PAIR / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
+               + c.P * GEMM2_FLOPS_PER_PAIR / (F16_PEAK_TFLOPS * 1e12)) * 1e6
     bound = "hbm" if hbm_us >= mfma_us else "mfma"
     floor = max(hbm_us, mfma_us)
     return {"bound": bound, "floor_us": round(floor, 1), "hbm_floor_us": round(hbm_us, 1),
@@ -287,7 +287,7 @@ MFMA_PASS_CASES = ("prefill_t8192", "skew_t4096")
 
 def mfma_pass(dev, weights_gpu, reps):
     """Launches for the MFMA counters (SQ_VALU_MFMA_BUSY_CYCLES with GRBM_GUI_ACTIVE,
-    SQ_INSTS_VALU_MFMA_MOPS_F8 / _BF16): `reps` operator calls of each large prefill
+    SQ_INSTS_VALU_MFMA_MOPS_F8 / _F16): `reps` operator calls of each large prefill
     configuration in turn, so the prefill GEMM kernels' dispatches come in that order."""
     cases = [Case(n, dev, weights_gpu) for n in MFMA_PASS_CASES]
     runner = Runner(dev, max(c.T for c in cases))
@@ -558,7 +558,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8e4m3 GEMM1 / bf16 GEMM2, fp32 accumulate",
+        "dtype": "fp8e4m3 GEMM1 / fp16 GEMM2 (e4m3 W2 widened exactly), fp32 accumulate",
         "data": "synthetic (seeded N(0,1) logits, N(0,0.1) bf16 bias, e4m3 block-quantised N(0,1) "
                 "activations and N(0,0.02) weights)",
         "config": {
