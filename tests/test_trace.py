@@ -36,6 +36,34 @@ def test_definition_is_the_operators():
     assert d["axes"]["gemm1_out_size"]["value"] == 2 * d["axes"]["intermediate_size"]["value"]
 
 
+REFERENCE_DEFINITION = "/root/reference/reference moe/ref_moe.json"
+
+
+def test_reference_definition_accepted():
+    """The reference's own definition file (reference moe/ref_moe.json:11-145) passes
+    check_definition unchanged, and agrees with definition_dict() on every field the
+    check reads."""
+    if not os.path.exists(REFERENCE_DEFINITION):
+        pytest.skip(f"{REFERENCE_DEFINITION} is not on this host (the reference tree is read here only)")
+    with open(REFERENCE_DEFINITION) as f:
+        ref = json.load(f)
+    trace.check_definition(ref)
+    mine = trace.definition_dict()
+    assert ref["name"] == mine["name"]
+    assert list(ref["inputs"]) == list(mine["inputs"])
+    for n in mine["inputs"]:
+        assert (ref["inputs"][n]["shape"], ref["inputs"][n]["dtype"]) == \
+            (mine["inputs"][n]["shape"], mine["inputs"][n]["dtype"]), n
+    for k, v in mine["axes"].items():
+        assert ref["axes"][k]["type"] == v["type"], k
+        if v["type"] == "const":
+            assert ref["axes"][k]["value"] == v["value"], k
+    broken = copy.deepcopy(ref)
+    broken["inputs"]["hidden_states_scale"]["shape"] = ["seq_len", "num_hidden_blocks"]
+    with pytest.raises(trace.TraceFormatError):
+        trace.check_definition(broken)
+
+
 @pytest.mark.parametrize("edit", [
     lambda d: d.update(name="other_op"),
     lambda d: d["axes"]["hidden_size"].update(value=4096),
