@@ -25,7 +25,7 @@ hipError_t launch_router_quantize(const uint16_t*, const uint16_t*, int, float*,
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const int32_t*,
                                const float*, int, uint16_t*, hipStream_t);
 int gemm1_decode_blocks_per_cu();
-hipError_t launch_gemm1_loader(const uint8_t*, const float*, int, const uint8_t*, const float*,
+hipError_t launch_gemm1_prefill(const uint8_t*, const float*, int, const uint8_t*, const float*,
                                const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
                                float*, int, hipStream_t);
@@ -166,7 +166,7 @@ hipError_t run_stage(int stage, const Call& c) {
                                    c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr, c.perm_tok, c.perm_w,
                                    c.tok_pair, c.c_act, grid, c.stream);
       }
-      return launch_gemm1_loader(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
+      return launch_gemm1_prefill(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
                                  (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
       if (c.decode) return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_tok, c.perm_w, c.T, c.out, c.stream);

@@ -23,18 +23,21 @@
 //                (active expert, 8-column) items. GEMM2: workgroup c owns 28
 //                output columns of every active expert and sums each token's
 //                pairs itself, writing bf16 rows (no combine kernel).
-//   *_loader  -- many rows per expert (prefill). Persistent workgroups walk a
-//                device-built list of (expert, row tile, column tile) items;
-//                loader waves move operands global -> LDS with direct loads into
-//                a ring of stages, in the exact order the MFMA reads them, while
-//                compute waves run the MFMAs. The workgroups of one XCD take
-//                consecutive items, which share the weight tile, so that XCD's
-//                L2 serves the repeats.
+//   prefill   -- many rows per expert. Persistent workgroups walk a device-built
+//                list of (expert, row tile, column tile) items, moving operands
+//                global -> LDS with direct loads into a ring of stages, in the
+//                exact order the MFMA reads them. GEMM1 (gemm1_prefill_kernel):
+//                every wave computes and issues direct loads from inline asm.
+//                GEMM2 (gemm2_loader_kernel): loader waves issue the direct loads
+//                while compute waves run the MFMAs. The workgroups of one XCD take
+//                consecutive items, which share operand tiles, so that XCD's L2
+//                serves the repeats.
 #include "moe_common.h"
 #include "moe_host.h"
 #include "moe_route_token.h"
 #include "moe_small_dispatch.h"
 #include "moe_tile.h"
+#include "../../include/moe_fp8.h"
 
 namespace moe {
 
@@ -619,18 +622,19 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
 // ---------------------------------------------------------------------------
 // Items of the tiled (prefill) kernels: (row tile, column tile) pairs.
 //
-// Row tiles are BM = 128 rows of one expert's segment, numbered expert by
-// expert in descending order of the experts' row counts (ties: lower id first),
-// each expert's tiles in row order. All tiles of an expert share its weight
-// tiles, which stay in the caches while they run; the largest experts (whose
-// tiles are full and cost the most: the compute waves skip row fragments past
-// the valid count) come first, and the one-tile experts with few rows, the
-// cheapest items, last, where they even out the workgroups' finishing times.
-// The block order: blocks of 8 row tiles x 4 column tiles, row-block major.
+// Row tiles are BM rows of one expert's segment (GEMM1: 256, GEMM2: 128),
+// numbered expert by expert in descending order of the experts' row counts
+// (ties: lower id first), each expert's tiles in row order. All tiles of an
+// expert share its weight tiles, which stay in the caches while they run; the
+// largest experts (whose tiles are full and cost the most: the waves skip row
+// fragments past the valid count) come first, and the one-tile experts with few
+// rows, the cheapest items, last, where they even out the workgroups' finishing
+// times. The block order: blocks of TBM row tiles x TBN column tiles (GEMM1 4 x 8,
+// GEMM2 8 x 4), row-block major.
 //
 // Both kernels deal the block order statically in rounds (snake_item): each
-// 32-item block runs on the 32 workgroups of one XCD in step, sharing its 8
-// activation and 4 weight tiles in that XCD's L2. (Handing the items out at run
+// 32-item block runs on the 32 workgroups of one XCD in step, sharing its
+// activation and weight tiles in that XCD's L2. (Handing the items out at run
 // time from per-XCD atomic work queues was measured: slower for GEMM1, whose
 // workgroups then drift apart so that the L2 stops serving the repeats, and no
 // faster for GEMM2.)
@@ -717,270 +721,404 @@ __device__ __forceinline__ int snake_item(int r, int slot, int G) { return r * G
 
 
 // ---------------------------------------------------------------------------
-// GEMM1 + SwiGLU, prefill shape: 128 rows x 128 column pairs (X1 rows n..n+127
-// and X2 rows 2048+n..) per item. 8 compute waves as 2 (rows) x 4 (pairs); each
-// owns 64 rows (the 16-row fragments 2 mt + wm, mt < 4, so the two row halves
-// interleave) x 32 pairs = 4 x 4 MFMA tiles (2 X1 + 2 X2 column tiles), and 4
-// loader waves move the operands.
-//
-// Operands go global -> LDS with the direct load (global_load_lds_dwordx4):
-// one wave instruction moves 64 lanes x 16 B and lane l's bytes land at
-// base + 16 l, with no staging registers. Each instruction loads 8 whole
-// 128 B row lines of a K block; the 16 B chunks are XOR-swizzled per row so
-// that the MFMA fragment reads (lds_frag_sw) are conflict-free. The activation
-// scales of the item's rows and the two weight block scales ride along.
-// Three LDS stages: the loads for K block kb+2 fly while kb computes.
-// ---------------------------------------------------------------------------
-constexpr int FRAG_BYTES = 2048;           // one 16 x 128 e4m3 fragment
-constexpr int Q1_BM = 128;
-constexpr int Q1_BNP = 128;
-constexpr int Q1_NT = I / Q1_BNP;          // 16 column-pair tiles
-constexpr int Q1_AFR = Q1_BM / 16;         // 8 activation fragments per stage
-constexpr int Q1_BFR = 2 * Q1_BNP / 16;    // 16 weight fragments per stage (0-7 X1, 8-15 X2)
-constexpr int Q1_SCALE_OFF = (Q1_AFR + Q1_BFR) * FRAG_BYTES;
-constexpr int Q1_NSTAGE = 3;
+// One 16 x 128 e4m3 MFMA fragment in LDS (two 1 KB halves of 8 rows each).
+constexpr int FRAG_BYTES = 2048;
 
 // ---------------------------------------------------------------------------
-// Why loader waves: when every wave issued its own share of the loads right
-// after each K block's barrier, a wave waiting to issue loads into a busy
-// memory pipeline held back its MFMAs, and load time added to compute time.
-// With the global -> LDS traffic issued by 4 loader waves, the 8 compute waves
-// only read LDS and run MFMAs and the scale FMAs, and the 3-slot ring runs on
-// across items (the loaders fill the next item's first stages while the
-// compute waves finish the current one). One barrier per K
-// block: before it, each loader wave has waited for its own loads of that
-// block, each compute wave for its reads of the previous one.
+// GEMM1 + SwiGLU, prefill shape: items of 256 rows x 128 column pairs (X1 rows
+// n..n+127 and X2 rows 2048+n..), so an expert with up to 256 rows reads each
+// weight byte once. 8 waves as 4 (row groups) x 2 (column halves): wave (wm,
+// wn) owns the 16-row fragments 4 mt + wm (mt < 4; the groups interleave, so a
+// partly filled tile spreads its valid fragments evenly over the waves) against
+// 4 X1 and 4 X2 column fragments: 32 MFMAs of 16x16x128 per K block into 128
+// fp32 accumulators. Fragments past the valid rows are skipped, and so are the
+// direct loads of activation rows past them.
 //
-// Loader wave p (0..3) moves, per K block, activation rows 32 p .. 32 p + 31
-// (4 half fragments), 8 of the 32 weight half fragments and the 32 activation
-// scales of its rows; the last one also the block's two weight scales (X1 and
-// X2 block rows), so the compute waves take every operand from LDS (a scalar
-// load in their loop would make them wait for all their LDS reads). Its rows' token indices come from scalar loads of
-// perm_tok: the 32 entries from row 32 p of the tile may run past the expert's
-// segment (up to 127 entries past the end of perm_tok, which the workspace
-// follows with the perm_w and C regions), and every row at or past the tile's
-// valid count takes the tile's first token instead.
+// Every wave computes, and every wave moves an eighth of each K block global ->
+// LDS with direct loads into a ring of stages. An item with more than 128 valid
+// rows uses 2 stages of 66 KB (the loads of block kb+1 fly while kb computes);
+// one with at most 128 uses 3 stages of 50 KB (its activation part is half as
+// large), so the loads of kb+2 fly while kb computes: such items do little MFMA
+// work per block and would otherwise wait for an HBM round trip every block.
+// The direct loads are issued from inline asm: the compiler does not track them,
+// so it puts no wait for them before the fragment reads of the other stages (for
+// the builtin it waits for every direct load in flight before any LDS read, which
+// is why a design built on the builtin needs loader waves that never read LDS,
+// and loses a third of the register file to them). The kernel waits for its own
+// loads explicitly (s_waitcnt vmcnt) before the barrier that ends every K block.
+// M0, which the direct load takes its LDS address from, is set in the same asm
+// statement; nothing else in this kernel uses M0.
+//
+// The waves issue their direct loads at two points of the block: waves 0-3 at its
+// top, waves 4-7 halfway through their MFMAs, so the two waves of a SIMD (w,
+// w + 4) take turns. Issued by all waves at the top of the block they held every
+// wave there for ~1,000 clk (the CU moves about 64 B/clk from L2 into LDS, 64 KB
+// per block); split, the loads of one half run beside the other half's MFMAs,
+// and a wave stalled on a full load queue leaves its SIMD to the other wave.
+//
+// Per K block and row the fp32 factors s_act[row, kb] * s_w[X1 or X2 block, kb]
+// are formed once (wave w: row 64 (w % 4) + lane, X1 for w < 4, X2 above) and
+// stored in the stage beside the operands as (X1, X2) pairs, one block ahead; the
+// activation scales and the two weight block scales arrive two blocks ahead by
+// direct loads into a small LDS buffer.
 // ---------------------------------------------------------------------------
-constexpr int W1_CWAVES = 8;
-constexpr int W1_PWAVES = 4;
-constexpr int W1_THREADS = 64 * (W1_CWAVES + W1_PWAVES);
-constexpr int W1_AJOBS = 2 * Q1_AFR / W1_PWAVES;  // 4
-constexpr int W1_BJOBS = 2 * Q1_BFR / W1_PWAVES;  // 8
-constexpr int W1_WSCALE_OFF = Q1_SCALE_OFF + Q1_BM * 4;  // the two weight block scales of the K block
-constexpr int W1_STAGE = W1_WSCALE_OFF + 16;
-static_assert(W1_AJOBS == 4 && W1_BJOBS == 8 && Q1_BM == 32 * W1_PWAVES, "loader split");
+constexpr int P1_BM = 256;
+constexpr int P1_BNP = 128;
+constexpr int P1_NT = I / P1_BNP;          // 16 column-pair tiles
+constexpr int P1_WAVES = 8;
+constexpr int P1_THREADS = 64 * P1_WAVES;
+constexpr int P1_B_BYTES = 2 * P1_BNP * BLK;  // 32 KB: 16 weight fragments (0-7 X1, 8-15 X2)
+constexpr int P1_F_BYTES = 2 * P1_BM * 4;     // (X1, X2) factor pairs of the 256 rows
+template <int NST>
+struct P1Ring {  // the stage layout of an NST-stage ring
+  static constexpr int A_BYTES = (NST == 2 ? P1_BM : P1_BM / 2) * BLK;
+  static constexpr int B_OFF = A_BYTES;
+  static constexpr int F_OFF = A_BYTES + P1_B_BYTES;
+  static constexpr int STAGE = F_OFF + P1_F_BYTES;
+  static constexpr int BYTES = NST * STAGE;
+};
+constexpr int P1_SA_OFF = P1Ring<2>::BYTES > P1Ring<3>::BYTES ? P1Ring<2>::BYTES : P1Ring<3>::BYTES;
+constexpr int P1_SA_BUF = P1_BM * 4 + 16;  // activation scales of the 256 rows, then the X1 and X2 weight scales
+constexpr int P1_LDS = P1_SA_OFF + 2 * P1_SA_BUF;
+constexpr int P1_TBM = 4, P1_TBN = 8;  // 32-item blocks: 4 row tiles x 8 column tiles
+static_assert(P1_BM * BLK == 4 * P1_WAVES * 1024 && P1_B_BYTES == 4 * P1_WAVES * 1024,
+              "4 half fragments of each operand per wave");
+static_assert(P1_NT % P1_TBN == 0 && P1_TBM * P1_TBN == 32, "block order");
+static_assert(P1_LDS + (int)sizeof(TileMap) <= 160 * 1024, "LDS");
+static_assert((size_t)MOE_FP8_MAX_TOKENS * H < (1ull << 32) && (size_t)E_LOCAL * N1 * H < (1ull << 32) &&
+                  (size_t)E_LOCAL * NB_N1 * NB_H * 4 < (1ull << 32),
+              "32-bit load offsets");
 
-// Spread scalar values over lanes: lane l of the result holds t[base + (l >> shift)]
-// for l < lanes (one v_writelane per lane; a select chain would be turned into an
-// indexed scratch table, whose loads count in vmcnt like the direct loads).
-// v_writelane ignores EXEC, so this must run in uniform control flow with every
-// lane active: the asm is volatile so that the compiler cannot sink it into a
-// divergent branch (where it would overwrite the inactive lanes too), and callers
-// compute every spread before any per-lane select of the results.
-template <int LANES, int SHIFT>
-__device__ __forceinline__ int spread_lanes(const int (&t)[32], int base) {
-  int v = 0;
-#pragma unroll
-  for (int l = 0; l < LANES; ++l)
-    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(t[base + (l >> SHIFT)]), "i"(l));
-  return v;
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
-// One item's 56 K blocks for a compute wave of the GEMM1 loader kernel: NMT of
-// its 16-row fragments (2 mt + wm, mt < NMT) against its 2 X1 and 2 X2 column
-// tiles. Fragments past the item's valid rows are skipped (their rows would be
-// discarded), so a partly filled tile costs MFMA and scale work in proportion
-// to its rows; the interleaved fragment order keeps the two row halves' waves,
-// which sit on different SIMDs, within one fragment of each other. Every wave
-// takes the barrier of every K block whatever its NMT.
-template <int NMT>
-__device__ __forceinline__ void g1_loader_kloop(const uint8_t* q1_lds, int& slot, int wm, int wn, int kg, int flo,
-                                                int fhi, v4f (&accu)[4][2], v4f (&accg)[4][2]) {
+// Direct global -> LDS loads of 16 (4) B per lane from base + voff; lane l's bytes
+// land at lds + 16 l (4 l). Untracked by the compiler (see above). s_nop 4 covers
+// the wait states after an M0 write and after a VALU write of the base SGPRs.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, const uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+               "s"(lds_addr(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, const uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base),
+               "s"(lds_addr(lds))
+               : "memory");
+}
+
+// Loads of 4 token indices that the compiler does not track, waited for in the
+// same asm statement: for a tracked load the compiler would also wait, before the
+// first direct load that uses the result, for every direct load in flight.
+__device__ __forceinline__ void ld_sync4(const int32_t* p0, const int32_t* p1, const int32_t* p2, const int32_t* p3,
+                                         int& v0, int& v1, int& v2, int& v3) {
+  asm volatile(
+      "global_load_dword %0, %4, off\n\tglobal_load_dword %1, %5, off\n\t"
+      "global_load_dword %2, %6, off\n\tglobal_load_dword %3, %7, off\n\ts_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+      : "memory");
+}
+
+__device__ __forceinline__ void ld_sync1(const int32_t* p, int& v) {
+  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+}
+
+// The static deal of block_order_item with the block shape as a parameter.
+template <int BMT, int BNT>
+__device__ __forceinline__ int block_order_item_t(int i, int total_m, int nt_count) {
+  const int nbk = nt_count / BNT, nrb = (total_m + BMT - 1) / BMT;
+  const int full = (nrb - 1) * nbk * BMT * BNT;
+  int rb, cb, ii, rows;
+  if (i < full) {
+    const int b = i / (BMT * BNT);
+    rb = b / nbk;
+    cb = b % nbk;
+    ii = i % (BMT * BNT);
+    rows = BMT;
+  } else {
+    rows = total_m - BMT * (nrb - 1);
+    rb = nrb - 1;
+    cb = (i - full) / (rows * BNT);
+    ii = (i - full) % (rows * BNT);
+  }
+  return (BMT * rb + ii % rows) * nt_count + BNT * cb + ii / rows;
+}
+
+struct P1Item {
+  int e, m0, valid, nt, seg;
+};
+
+// Item of round r of this workgroup (false past the end). All values uniform.
+__device__ __forceinline__ bool p1_item(const TileMap& map, int r, int slot, int G, int total, P1Item& it) {
+  const int i = snake_item(r, slot, G);
+  if (i >= total) return false;
+  const int id = block_order_item_t<P1_TBM, P1_TBN>(i, map.total_m, P1_NT);
+  const int k = id / P1_NT;
+  int e, m0;
+  tile_row<P1_BM>(map, k, e, m0);
+  // values read from LDS are held per lane unless made scalar
+  it.e = __builtin_amdgcn_readfirstlane(e);
+  it.m0 = __builtin_amdgcn_readfirstlane(m0);
+  it.nt = __builtin_amdgcn_readfirstlane(id - k * P1_NT);
+  it.valid = __builtin_amdgcn_readfirstlane(min(P1_BM, map.cnt[it.e] - it.m0));
+  it.seg = __builtin_amdgcn_readfirstlane(map.seg[it.e]);
+  return true;
+}
+
+// Address of the token of tile row r; rows at or past the valid count take the first.
+__device__ __forceinline__ const int32_t* p1_token_ptr(const int32_t* perm_tok, const P1Item& it, int r) {
+  return perm_tok + it.seg + it.m0 + (r < it.valid ? r : 0);
+}
+
+struct P1Ctx {
+  const uint8_t* hidden;
+  const float* hscale;
+  int T;
+  const uint8_t* w13;
+  const float* s13;
+  uint16_t* c_act;
+  int w, lane, wm, wn, fr, kg, flo, fhi, frow, fkind;
+};
+
+// One wave's loads of one item, as byte offsets: A half fragments 4 w + j (tile
+// rows 32 w + 8 j + l / 8, from hidden) and B half fragments 4 w + j (fragment
+// f = (4 w + j) / 2: X1 rows 128 nt + 16 f + ..., X2 rows for f >= 8, from w13),
+// 16 B chunk (l % 8) ^ (l / 8) ^ half, without the K block's 128 B; the
+// activation-scale row (waves 0-3, from hscale) and the X1 / X2 weight-scale rows
+// (wave 4 lanes 0 / 1, from s13).
+struct P1Src {
+  uint32_t a[4], b[4];
+  int na;          // A half fragments holding valid rows (uniform)
+  uint32_t sa;     // activation scale of row 64 w + lane (waves 0-3)
+  uint32_t sw;     // weight-scale row (wave 4, lanes 0 and 1)
+};
+
+__device__ __forceinline__ void p1_src(const P1Ctx& x, const int32_t* perm_tok, const P1Item& it, P1Src& s) {
+  const int rr = x.lane >> 3;
+  int tok[4], tsa;
+  ld_sync4(p1_token_ptr(perm_tok, it, 32 * x.w + rr), p1_token_ptr(perm_tok, it, 32 * x.w + 8 + rr),
+           p1_token_ptr(perm_tok, it, 32 * x.w + 16 + rr), p1_token_ptr(perm_tok, it, 32 * x.w + 24 + rr), tok[0],
+           tok[1], tok[2], tok[3]);
+  ld_sync1(p1_token_ptr(perm_tok, it, x.frow), tsa);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = 4 * x.w + j, half = h & 1, c = (x.lane & 7) ^ rr ^ half;
+    s.a[j] = (uint32_t)tok[j] * H + c * 16;
+    const int f = h >> 1;
+    const int row = (f < 8 ? it.nt * P1_BNP + 16 * f : I + it.nt * P1_BNP + 16 * (f - 8)) + 8 * half + rr;
+    s.b[j] = ((uint32_t)it.e * N1 + row) * H + c * 16;
+  }
+  s.na = min(4, max(0, (it.valid - 32 * x.w + 7) / 8));
+  s.sa = (uint32_t)tsa * 4;
+  s.sw = ((uint32_t)it.e * NB_N1 + ((x.lane & 1) ? NB_I + it.nt : it.nt)) * NB_H * 4;
+}
+
+// Scales of block kb into SA buffer kb % 2.
+__device__ __forceinline__ void p1_scales(const P1Ctx& x, const P1Src& s, uint8_t* lds, int kb) {
+  uint8_t* sb = lds + P1_SA_OFF + (kb & 1) * P1_SA_BUF;
+  if (x.w < 4) dma4(x.hscale + (size_t)kb * x.T, s.sa, sb + 256 * x.w);
+  if (x.w == 4 && x.lane < 2) dma4(x.s13 + kb, s.sw, sb + P1_BM * 4);
+}
+
+// This wave's factor of block kb (its scales are in SA buffer kb % 2) into the
+// factor region f of the block's stage.
+__device__ __forceinline__ void p1_factor(const P1Ctx& x, const uint8_t* lds, uint8_t* f, int kb) {
+  const uint8_t* sb = lds + P1_SA_OFF + (kb & 1) * P1_SA_BUF;
+  const float sa = reinterpret_cast<const float*>(sb)[x.frow];
+  const float sw = reinterpret_cast<const float*>(sb + P1_BM * 4)[x.fkind];
+  reinterpret_cast<float*>(f)[2 * x.frow + x.fkind] = sa * sw;
+}
+
+// This wave's operand loads of block kb into the stage at st.
+template <int B_OFF>
+__device__ __forceinline__ void p1_operands(const P1Ctx& x, const P1Src& s, uint8_t* st, int kb) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j < s.na) dma16(x.hidden + kb * BLK, s.a[j], st + (4 * x.w + j) * 1024);
+    dma16(x.w13 + kb * BLK, s.b[j], st + B_OFF + (4 * x.w + j) * 1024);
+  }
+}
+
+// One K block of a wave: NMT valid token fragments (4 mt + wm) x 4 X1 + 4 X2 weight
+// fragments, accumulated with the stage's factors. The weight fragment is the
+// MFMA's first operand, so lane l's four results are weight columns 4 (l / 16) + r
+// of one token (l % 16), and the token's two factors (X1, X2) are one 8-byte LDS
+// read per fragment. The next block's operand loads (load(), when any) go out
+// before column group DMA_AT; for DMA_AT > 0 empty asm statements that read the
+// earlier groups' accumulators come first: asm volatile statements keep their
+// order, so those groups' MFMAs stay above the loads (without them the
+// instruction DAG sinks every MFMA below the loads).
+template <int NMT, int DMA_AT, int B_OFF, int F_OFF, typename Load>
+__device__ __forceinline__ void p1_block(const P1Ctx& x, const uint8_t* st, v4f (&au)[4][4], v4f (&ag)[4][4],
+                                         const Load& load) {
+  v8i a[NMT];
+  v2f f[NMT];
+#pragma unroll
+  for (int mt = 0; mt < NMT; ++mt) {
+    a[mt] = lds_frag_sw(st + (4 * mt + x.wm) * FRAG_BYTES, x.flo, x.fhi);
+    f[mt] = *reinterpret_cast<const v2f*>(st + F_OFF + ((4 * mt + x.wm) * 16 + x.fr) * 8);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (c == DMA_AT) {
+#pragma unroll
+      for (int cc = 0; cc < DMA_AT; ++cc)
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) asm volatile("" ::"v"(au[mt][cc]), "v"(ag[mt][cc]));
+      load();
+    }
+    const v8i bu = lds_frag_sw(st + B_OFF + (4 * x.wn + c) * FRAG_BYTES, x.flo, x.fhi);
+    const v8i bg = lds_frag_sw(st + B_OFF + (8 + 4 * x.wn + c) * FRAG_BYTES, x.flo, x.fhi);
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt) {
+      const v4f pu = mfma_fp8_k128(bu, a[mt]);
+      const v4f pg = mfma_fp8_k128(bg, a[mt]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        au[mt][c][r] += pu[r] * f[mt][0];
+        ag[mt][c][r] += pg[r] * f[mt][1];
+      }
+    }
+  }
+}
+
+// s_waitcnt vmcnt(n) for a uniform n in 0..8.
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+  }
+}
+
+// One item on an NST-stage ring (a wave with NMT valid token fragments): the
+// prologue fills stages 0..NST-2 and the scales of blocks 0 and 1, then each
+// block kb computes from stage kb % NST while its waves load block kb + NST - 1.
+// Before the barrier that ends block kb each wave waits for all its loads but
+// those of block kb + NST - 1 (loads complete in order; the scale loads of the
+// block are issued before them), so block kb + 1's operands and kb + 2's scales
+// are in place.
+template <int NMT, int DMA_AT, int NST>
+__device__ __forceinline__ void p1_run_item(const P1Ctx& x, const P1Item& ic, const P1Src& s, uint8_t* lds) {
+  using R = P1Ring<NST>;
+#pragma unroll
+  for (int b = 0; b < NST - 1; ++b) p1_operands<R::B_OFF>(x, s, lds + b * R::STAGE, b);
+  p1_scales(x, s, lds, 0);
+  p1_scales(x, s, lds, 1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  p1_factor(x, lds, lds + R::F_OFF, 0);
+  lds_barrier();
+
+  v4f au[4][4], ag[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      au[mt][c] = v4f{0.f, 0.f, 0.f, 0.f};
+      ag[mt][c] = au[mt][c];
+    }
+  const int n_ld = s.na + 4;  // direct loads of this wave per block
+  int cur = 0;
 #pragma unroll 1
   for (int kb = 0; kb < NB_H; ++kb) {
-    __builtin_amdgcn_s_barrier();  // K block kb is in its slot; the slot before it is free
-    asm volatile("" ::: "memory");
-    const uint8_t* st = q1_lds + slot * W1_STAGE;
-    slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
+    const int nxt = cur == NST - 1 ? 0 : cur + 1;          // stage of block kb + 1
+    const int ld = NST == 2 ? nxt : (nxt == NST - 1 ? 0 : nxt + 1);  // stage of block kb + NST - 1
+    if (kb + 1 < NB_H) p1_factor(x, lds, lds + nxt * R::STAGE + R::F_OFF, kb + 1);
+    if (kb + 2 < NB_H) p1_scales(x, s, lds, kb + 2);
+    const int kl = kb + NST - 1;
+    const bool loading = kl < NB_H;
+    auto load = [&]() {
+      if (loading) p1_operands<R::B_OFF>(x, s, lds + ld * R::STAGE, kl);
+    };
     if constexpr (NMT > 0) {
-      v8i a[NMT];
-#pragma unroll
-      for (int mt = 0; mt < NMT; ++mt) a[mt] = lds_frag_sw(st + (2 * mt + wm) * FRAG_BYTES, flo, fhi);
-      v4f pu[NMT][2], pg[NMT][2];
-#pragma unroll
-      for (int n2 = 0; n2 < 2; ++n2) {
-        const v8i bu = lds_frag_sw(st + (Q1_AFR + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
-        const v8i bg = lds_frag_sw(st + (Q1_AFR + Q1_BFR / 2 + wn * 2 + n2) * FRAG_BYTES, flo, fhi);
-#pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) {
-          pu[mt][n2] = mfma_fp8_k128(a[mt], bu);
-          pg[mt][n2] = mfma_fp8_k128(a[mt], bg);
-        }
-      }
-      const float swu = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF);
-      const float swg = *reinterpret_cast<const float*>(st + W1_WSCALE_OFF + 4);
+      p1_block<NMT, DMA_AT, R::B_OFF, R::F_OFF>(x, lds + cur * R::STAGE, au, ag, load);
+    } else {
+      load();
+    }
+    if (kb == NB_H - 1) {
+      // SwiGLU and the fp16 C rows (lane l: token row 16 (4 mt + wm) + l % 16, four
+      // consecutive columns from 4 (l / 16) of each of its 4 column fragments)
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
-        const v4f sa = *reinterpret_cast<const v4f*>(st + Q1_SCALE_OFF + ((2 * mt + wm) * 16 + 4 * kg) * 4);
-        v4f fu, fg;
+        const int row = (4 * mt + x.wm) * 16 + x.fr;
+        if (row < ic.valid) {
+          uint16_t* dst = x.c_act + (size_t)(ic.seg + ic.m0 + row) * I + ic.nt * P1_BNP + 4 * x.kg;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) { fu[r] = sa[r] * swu; fg[r] = sa[r] * swg; }
-#pragma unroll
-        for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            accu[mt][n2][r] += pu[mt][n2][r] * fu[r];
-            accg[mt][n2][r] += pg[mt][n2][r] * fg[r];
+          for (int c = 0; c < 4; ++c) {
+            uint2 v;
+            v.x = (uint32_t)c_encode(silu_mul(au[mt][c][0], ag[mt][c][0])) |
+                  ((uint32_t)c_encode(silu_mul(au[mt][c][1], ag[mt][c][1])) << 16);
+            v.y = (uint32_t)c_encode(silu_mul(au[mt][c][2], ag[mt][c][2])) |
+                  ((uint32_t)c_encode(silu_mul(au[mt][c][3], ag[mt][c][3])) << 16);
+            *reinterpret_cast<uint2*>(dst + (4 * x.wn + c) * 16) = v;
           }
+        }
       }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+    if (NST == 2 || !loading)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else
+      wait_vm(n_ld);
+    lds_barrier();
+    cur = nxt;
   }
 }
 
-__global__ __launch_bounds__(W1_THREADS, 1) void gemm1_loader_kernel(
-    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr,
-    const int32_t* __restrict__ perm_tok, uint16_t* __restrict__ c_act) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t q1_lds[];
+template <int DMA_AT>
+__device__ __forceinline__ void p1_dispatch(const P1Ctx& x, const P1Item& ic, const P1Src& s, uint8_t* lds) {
+  const int nf = (ic.valid + 15) / 16;
+  const int nmt = nf > x.wm ? (nf - x.wm + 3) / 4 : 0;
+  if (ic.valid > P1_BM / 2) {  // nf >= 9: nmt >= 2
+    switch (nmt) {
+      case 2: p1_run_item<2, DMA_AT, 2>(x, ic, s, lds); break;
+      case 3: p1_run_item<3, DMA_AT, 2>(x, ic, s, lds); break;
+      default: p1_run_item<4, DMA_AT, 2>(x, ic, s, lds); break;
+    }
+  } else {  // nf <= 8: nmt <= 2
+    switch (nmt) {
+      case 0: p1_run_item<0, DMA_AT, 3>(x, ic, s, lds); break;
+      case 1: p1_run_item<1, DMA_AT, 3>(x, ic, s, lds); break;
+      default: p1_run_item<2, DMA_AT, 3>(x, ic, s, lds); break;
+    }
+  }
+}
+
+__global__ __launch_bounds__(P1_THREADS, 1) void gemm1_prefill_kernel(
+    const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T, const uint8_t* __restrict__ w13,
+    const float* __restrict__ s13, const DispatchHeader* __restrict__ hdr, const int32_t* __restrict__ perm_tok,
+    uint16_t* __restrict__ c_act) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t p1_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  build_tile_map<Q1_BM>(hdr, map);
-  const int total = __builtin_amdgcn_readfirstlane(map.total_m) * Q1_NT, G = gridDim.x;
-  const int my_slot = xcd_remap(blockIdx.x, G);
-
-  if (wave >= W1_CWAVES) {
-    // ----------------------------- loader waves -----------------------------
-    const int p = wave - W1_CWAVES, rr = lane >> 3;
-    // the tile map in registers (lane e < 32 holds expert e's values), read before any
-    // direct load is in flight: later LDS reads would wait for every load in flight
-    const int my_pref = lane < E_LOCAL ? map.pref[lane] : 0;
-    const int my_next = lane < E_LOCAL ? map.pref[lane + 1] : 0x7fffffff;
-    const int my_order = lane < E_LOCAL ? map.order[lane] : 0;
-    const int my_cnt = lane < E_LOCAL ? map.cnt[lane] : 0;
-    const int my_seg = lane < E_LOCAL ? map.seg[lane] : 0;
-    const int map_total_m = __builtin_amdgcn_readfirstlane(map.total_m);
-    const uint8_t* srcA[W1_AJOBS];
-    const uint8_t* srcB[W1_BJOBS];
-    const float* ssrc = hscale;
-    int sstride = T;
-    const bool scale_lane = lane < 32 || (p == W1_PWAVES - 1 && lane < 34);
-    int round = -1, kb = NB_H, slot = 0, issued = 0;
-    bool more = true;
-
-    auto next_item = [&]() -> bool {
-      const int i = snake_item(++round, my_slot, G);
-      if (i >= total) return false;
-      const int it = block_order_item(i, map_total_m, Q1_NT);
-      const int k = it / Q1_NT, nt = it % Q1_NT;
-      const int j = __popcll(__ballot(my_next <= k));  // ranks whose tiles all lie before k
-      const int e = __builtin_amdgcn_readlane(my_order, j);
-      const int m0 = (k - __builtin_amdgcn_readlane(my_pref, j)) * Q1_BM;
-      const int cnt = __builtin_amdgcn_readlane(my_cnt, e), seg = __builtin_amdgcn_readlane(my_seg, e);
-      const int valid = min(Q1_BM, cnt - m0);
-      const int32_t* tp = perm_tok + seg + m0;
-      int tk[32];
-#pragma unroll
-      for (int j = 0; j < 32; ++j) tk[j] = tp[32 * p + j];
-      const int tok0 = tp[0];
-      // every spread first, with all lanes active (see spread_lanes), then the
-      // per-lane choice: rows at or past the valid count take the first token
-      int spread[W1_AJOBS];
-#pragma unroll
-      for (int i = 0; i < W1_AJOBS; ++i) spread[i] = spread_lanes<64, 3>(tk, 8 * i);
-      const int spread_s = spread_lanes<32, 0>(tk, 0);
-#pragma unroll
-      for (int i = 0; i < W1_AJOBS; ++i) {
-        const int r = 8 * i + rr, jj = i & 1;
-        const int tok = 32 * p + r < valid ? spread[i] : tok0;
-        srcA[i] = hidden + (size_t)tok * H + ((lane & 7) ^ rr ^ jj) * 16;
-      }
-#pragma unroll
-      for (int i = 0; i < W1_BJOBS; ++i) {
-        const int g = 4 * p + (i >> 1), jj = i & 1;
-        const int row = (g < Q1_BFR / 2 ? nt * Q1_BNP + g * 16 : I + nt * Q1_BNP + (g - Q1_BFR / 2) * 16) + 8 * jj + rr;
-        srcB[i] = w13 + ((size_t)e * N1 + row) * H + ((lane & 7) ^ rr ^ jj) * 16;
-      }
-      const int q = lane & 31;
-      ssrc = hscale + (32 * p + q < valid ? spread_s : tok0);
-      sstride = T;
-      if (lane >= 32) {  // lanes 32, 33 of the last loader wave: X1 and X2 weight block scales
-        ssrc = s13 + ((size_t)e * NB_N1 + (lane == 32 ? nt : NB_I + nt)) * NB_H;
-        sstride = 1;
-      }
-      kb = 0;
-      return true;
-    };
-    auto issue = [&]() {
-      if (kb == NB_H && !(more = next_item())) return;
-      uint8_t* st = q1_lds + slot * W1_STAGE;
-#pragma unroll
-      for (int i = 0; i < W1_AJOBS; ++i)
-        lds_direct16(srcA[i] + kb * BLK, st + (2 * p + (i >> 1)) * FRAG_BYTES + (i & 1) * 1024);
-#pragma unroll
-      for (int i = 0; i < W1_BJOBS; ++i)
-        lds_direct16(srcB[i] + kb * BLK, st + (Q1_AFR + 4 * p + (i >> 1)) * FRAG_BYTES + (i & 1) * 1024);
-      // lane l lands at + 4 l: the wave's 32 row scales, then (last wave) the weight scales
-      if (scale_lane) lds_direct4(ssrc + (size_t)kb * sstride, st + Q1_SCALE_OFF + 128 * p);
-      slot = slot == Q1_NSTAGE - 1 ? 0 : slot + 1;
-      ++kb;
-      ++issued;
-    };
-    issue();
-    if (more) issue();
+  build_tile_map<P1_BM>(hdr, map);
+  P1Ctx x;
+  x.hidden = hidden; x.hscale = hscale; x.T = T; x.w13 = w13; x.s13 = s13; x.c_act = c_act;
+  x.w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  x.lane = lane;
+  x.wm = x.w & 3; x.wn = x.w >> 2; x.fr = lane & 15; x.kg = lane >> 4;
+  frag_sw_offsets(lane, x.flo, x.fhi);
+  x.frow = 64 * (x.w & 3) + lane;  // the factor row this wave forms
+  x.fkind = x.w >> 2;              // 0: X1, 1: X2
+  const int total = __builtin_amdgcn_readfirstlane(map.total_m) * P1_NT, G = gridDim.x;
+  const int slot = xcd_remap(blockIdx.x, G);
 #pragma unroll 1
-    for (int g = 0; g < issued; ++g) {
-      if (g + 1 < issued) asm volatile("s_waitcnt vmcnt(13)" ::: "memory");  // 13 loads per K block
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if (more) issue();
-    }
-    return;
-  }
-
-  // ------------------------------- compute waves -------------------------------
-  const int fr = lane & 15, kg = lane >> 4;
-  const int wm = wave & 1, wn = wave >> 1;
-  int flo, fhi;
-  frag_sw_offsets(lane, flo, fhi);
-  int slot = 0;
-  for (int round = 0;; ++round) {
-    const int i = snake_item(round, my_slot, G);
-    if (i >= total) break;
-    const int it = block_order_item(i, map.total_m, Q1_NT);
-    const int k = it / Q1_NT, nt = it % Q1_NT;
-    int e, m0;
-    tile_row<Q1_BM>(map, k, e, m0);
-    const int cnt = map.cnt[e], seg = map.seg[e];
-    // 16-row fragments holding valid rows; this wave's are 2 mt + wm for mt < nmt
-    const int nf = (min(Q1_BM, cnt - m0) + 15) / 16;
-    const int nmt = (nf + 1 - wm) / 2;
-    v4f accu[4][2], accg[4][2];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int n2 = 0; n2 < 2; ++n2) { accu[mt][n2] = v4f{0.f, 0.f, 0.f, 0.f}; accg[mt][n2] = accu[mt][n2]; }
-    switch (nmt) {
-      case 0: g1_loader_kloop<0>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
-      case 1: g1_loader_kloop<1>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
-      case 2: g1_loader_kloop<2>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
-      case 3: g1_loader_kloop<3>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
-      default: g1_loader_kloop<4>(q1_lds, slot, wm, wn, kg, flo, fhi, accu, accg); break;
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int n2 = 0; n2 < 2; ++n2)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + (2 * mt + wm) * 16 + 4 * kg + r;
-          if (row < cnt) {
-            const int col = nt * Q1_BNP + wn * 32 + n2 * 16 + fr;
-            c_act[(size_t)(seg + row) * I + col] = c_encode(silu_mul(accu[mt][n2][r], accg[mt][n2][r]));
-          }
-        }
+  for (int r = 0;; ++r) {
+    P1Item ic;
+    if (!p1_item(map, r, slot, G, total, ic)) break;
+    P1Src s;
+    p1_src(x, perm_tok, ic, s);
+    if (x.w < 4)
+      p1_dispatch<0>(x, ic, s, p1_lds);
+    else
+      p1_dispatch<2>(x, ic, s, p1_lds);
   }
 }
 
@@ -1346,17 +1484,17 @@ hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const f
   return hipGetLastError();
 }
 
-hipError_t launch_gemm1_loader(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
+hipError_t launch_gemm1_prefill(const uint8_t* hidden, const float* hscale, int T, const uint8_t* w13,
                                const float* s13, const DispatchHeader* hdr, const int32_t* perm_tok,
                                uint16_t* c_act, int grid, hipStream_t stream) {
   static PerDeviceOnce<hipError_t> once;
   hipError_t e = hipErrorInvalidDevice;
-  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_loader_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, Q1_NSTAGE * W1_STAGE); },
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_prefill_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, P1_LDS); },
            e);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(gemm1_loader_kernel, dim3(grid), dim3(W1_THREADS), Q1_NSTAGE * W1_STAGE, stream, hidden,
-                     hscale, T, w13, s13, hdr, perm_tok, c_act);
+  hipLaunchKernelGGL(gemm1_prefill_kernel, dim3(grid), dim3(P1_THREADS), P1_LDS, stream, hidden, hscale, T, w13,
+                     s13, hdr, perm_tok, c_act);
   return hipGetLastError();
 }
 
