@@ -789,8 +789,11 @@ static_assert((size_t)MOE_FP8_MAX_TOKENS * H < (1ull << 32) && (size_t)E_LOCAL *
                   (size_t)E_LOCAL * NB_N1 * NB_H * 4 < (1ull << 32),
               "32-bit load offsets");
 
+// LDS address of p as a scalar (the callers' addresses are uniform; inside a
+// lane-divergent branch the compiler may otherwise keep them in a VGPR, which the
+// asm's SGPR operand cannot take).
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p);
 }
 
 // Direct global -> LDS loads of 16 (4) B per lane from base + voff; lane l's bytes
