@@ -347,7 +347,8 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
     const int w = threadIdx.x >> 6;
     // tie scratch: the wave's activation stage, first written after the barrier below
     if (w < T)
-      route_token(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr, reinterpret_cast<TieScratch*>(&sh.a[w][0][0][0]));
+      route_token<false>(logits, bias, w, rsf, sh.d.ids, sh.d.wts, nullptr,
+                         reinterpret_cast<TieScratch*>(&sh.a[w][0][0][0]));
     lds_barrier();
     if (blockIdx.x == 0 && (int)threadIdx.x < T * TOP_K) {
       topk_ids[threadIdx.x] = sh.d.ids[threadIdx.x];

@@ -6,7 +6,9 @@
 //                     scaled). One wave64 per token, 4 experts per lane; the
 //                     top-8 by 8 rounds of wave arg-max, and the reference's
 //                     nth_element order where equal keys straddle a cut
-//                     (moe_route_token.h, moe_route_ties.h).
+//                     (moe_route_token.h, moe_route_ties.h). From 6,144 tokens
+//                     on, tokens first take the fast path (hardware exp/rcp
+//                     scores, cuts certified against their error bound).
 // dispatch_count_kernel, dispatch_scatter_kernel -- reference
 //                     moe/ref_moe.py:131-145 (for each local expert the ascending
 //                     list of tokens that selected it): per-chunk counts, then
@@ -19,6 +21,7 @@
 
 namespace moe {
 
+template <bool FAST>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
                                                     const uint16_t* __restrict__ bias, int T, float rsf,
                                                     int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
@@ -26,7 +29,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   __shared__ TieScratch tie[4];
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  route_token(logits, bias, t, rsf, topk_ids, topk_w, tok_pair, &tie[threadIdx.x >> 6]);
+  route_token<FAST>(logits, bias, t, rsf, topk_ids, topk_w, tok_pair, &tie[threadIdx.x >> 6]);
 }
 
 // Dispatch of up to 64 tokens in one workgroup with the same device code the
@@ -49,11 +52,17 @@ __global__ __launch_bounds__(SMALL_P) void dispatch_small_kernel(const int32_t* 
 // ---------------------------------------------------------------------------
 namespace moe {
 
+constexpr int kRouteFastMinTokens = 6144;  // 6 tokens per SIMD
+
 hipError_t launch_route(const float* logits, const uint16_t* bias, int T, float rsf, int32_t* topk_ids,
                         float* topk_w, int32_t* tok_pair, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias, T, rsf, topk_ids,
-                     topk_w, tok_pair);
+  if (T >= kRouteFastMinTokens)
+    hipLaunchKernelGGL(route_kernel<true>, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias, T, rsf, topk_ids,
+                       topk_w, tok_pair);
+  else
+    hipLaunchKernelGGL(route_kernel<false>, dim3((T + 3) / 4), dim3(256), 0, stream, logits, bias, T, rsf, topk_ids,
+                       topk_w, tok_pair);
   return hipGetLastError();
 }
 

@@ -4,6 +4,9 @@ Bars: expert selection and the per-expert permutation bit-exact; the bf16 output
 within atol=1e-2, rtol=2e-2 (torch.allclose semantics) of the reference.
 Everything goes through libmoe_mi355x.so's C ABI via flashinfer_mlsys_amd.
 """
+import ctypes
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -87,6 +90,65 @@ def test_route_ties_follow_torch_topk(dev, T):
     # every key equal: the reference keeps groups 4-7 and experts 168-175
     eq, _, _ = fm.route(torch.ones((T, 256), device=dev), torch.zeros(256, dtype=torch.bfloat16, device=dev), 2.5)
     assert (eq.cpu().numpy() == np.arange(168, 176, dtype=np.int32)).all()
+
+
+def _near_tie_tokens(T, seed):
+    """Token families that put the group and expert cuts anywhere from exact ties to
+    far apart: N(0,1) logits; logits on a grid c + k*2^-e (e in 12..24, so sigmoid
+    gaps of 0 to a few thousand fp32 ulps, around the fast path's certification
+    bound); the tie set; huge magnitudes (exp overflows / underflows, s = 0 or 1)."""
+    rng = np.random.default_rng(seed)
+    lg = rng.standard_normal((T, 256)).astype(np.float32)
+    fam = rng.integers(0, 4, size=T)
+    for t in np.nonzero(fam == 1)[0]:
+        e = int(rng.integers(12, 25))
+        c = np.float32(rng.uniform(-1.5, 1.5))
+        lg[t] = c + rng.integers(0, 64, size=256).astype(np.float32) * np.float32(2.0 ** -e)
+    tie = fam == 2
+    lg[tie] = TIE_LOGITS[rng.integers(0, len(TIE_LOGITS), size=(int(tie.sum()), 256))]
+    big = fam == 3
+    lg[big] = rng.choice(np.array([-200.0, -90.0, -30.0, 30.0, 90.0, 200.0], dtype=np.float32),
+                         size=(int(big.sum()), 256)) + lg[big]
+    return lg
+
+
+TEST_SUPPORT_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "libmoe_test_support.so")
+
+
+def test_fast_sigmoid_error_bound():
+    """The routing fast path certifies its cuts assuming |fast_sigmoid(x) -
+    exact_sigmoid(x)| <= 2^-20; the kernel here measures the largest difference over
+    every finite fp32 x with the routing kernels' own device functions."""
+    if not os.path.exists(TEST_SUPPORT_LIB):
+        raise FileNotFoundError(f"{TEST_SUPPORT_LIB} is not built (build() compiles it)")
+    lib = ctypes.CDLL(TEST_SUPPORT_LIB)
+    lib.moe_test_fast_sigmoid_max_error.argtypes = [ctypes.POINTER(ctypes.c_double)]
+    lib.moe_test_fast_sigmoid_max_error.restype = ctypes.c_int
+    out = ctypes.c_double(-1.0)
+    assert lib.moe_test_fast_sigmoid_max_error(ctypes.byref(out)) == 0
+    _say(f"max |fast_sigmoid - exact_sigmoid| = {out.value:.3e} = {out.value / 2.0 ** -23:.2f} * 2^-23")
+    assert 0.0 < out.value <= 2.0 ** -20
+
+
+@pytest.mark.parametrize("T,bias_kind", [(6144, "normal"), (6144, "tie"), (9000, "normal")])
+def test_route_fast_path_certification(dev, T, bias_kind):
+    """From 6,144 tokens the routing kernel tries the fast scores first and keeps
+    their selection only when both cuts clear the error bound; every other token
+    takes the exact path. Either way the selection must be the oracle's bit for bit
+    (exp correctly rounded, as the exact path) and the weights within a few ulps."""
+    lg = _near_tie_tokens(T, 97 + T)
+    rng = np.random.default_rng(T)
+    if bias_kind == "tie":
+        b = TIE_BIAS[rng.integers(0, len(TIE_BIAS), size=256)]
+    else:
+        b = (rng.standard_normal(256) * 0.1).astype(np.float32)
+    bias = torch.from_numpy(b).to(torch.bfloat16)
+    ids, w, _ = fm.route(torch.from_numpy(lg).to(dev), bias.to(dev), 2.5)
+    ref_idx, dense, _, _, _ = cpu_ref.route(torch.from_numpy(lg), bias, 2.5, exp="correctly_rounded")
+    ids = ids.cpu().numpy()
+    np.testing.assert_array_equal(ids, cpu_ref.sorted_selection(ref_idx).numpy().astype(np.int32))
+    np.testing.assert_allclose(w.cpu().numpy(), torch.gather(dense, 1, torch.from_numpy(ids).long()).numpy(),
+                               rtol=4e-7 * 8, atol=0)
 
 
 @pytest.mark.parametrize("case", ALL, indirect=True)
