@@ -1243,19 +1243,28 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
   }
-  // epilogue: weight by the pair's routing weight, one fp32 row per pair
+  // epilogue: weight by the pair's routing weight, one fp32 row per pair. The
+  // weights of a row block's 16 rows per lane are requested at once (rows past
+  // the valid ones read the last valid row's weight, unused), so its stores wait
+  // for one round trip, not one per row behind the stores before it.
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int i = 0; i < NI; ++i) {
+    float w[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
+      w[r] = perm_w[it.seg + min(row, it.cnt - 1)];
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
       if (row < it.cnt) {
-        const float w = perm_w[it.seg + row];
         float* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
+        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w[r];
       }
     }
+  }
 }
 
 __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
