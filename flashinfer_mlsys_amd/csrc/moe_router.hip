@@ -23,7 +23,11 @@
 // Larger T: LDS-staged tiles of 128 tokens x 64 experts, 8 compute waves of
 // 32 x 32 (v_mfma_f32_32x32x16_bf16) and 4 loader waves that stream each 128-wide
 // K block (hidden rows and gate rows, whole 128 B lines, 32-row swizzle) into a
-// 3-slot LDS ring two blocks ahead, as the prefill GEMM1 does.
+// 3-slot LDS ring two blocks ahead, as the prefill GEMM1 does. Between 576 tokens
+// and the token count whose 32-token items fill the CUs once (2,048 on 256 CUs),
+// router_ksplit_kernel: 32 x 64 tiles, a 5-slot ring, each K block's MFMA steps
+// split over the 8 compute waves and the four K quarters added in LDS in a
+// fixed order.
 #include "moe_common.h"
 #include "moe_host.h"
 #include "moe_tile.h"
@@ -222,6 +226,144 @@ __global__ __launch_bounds__(64 * (RT2_CWAVES + RT2_PWAVES), 1) void router_tile
   }
 }
 
+// Middle T (from RT2_MIN_T tokens while its items fit on the CUs: 2,048 tokens on
+// 256 CUs): the tiled kernel has fewer items than CUs there, and each item's 56 K
+// blocks pass a 3-slot ring one memory latency per two blocks (33-36 us whatever
+// T; 19-21 us here). Here an item is 32 tokens x 64 experts,
+// so four times as many workgroups take part, and its stage (24 KB: one 32-row
+// block of hidden rows, two of gate rows) fits a 5-slot ring, four blocks ahead.
+// The 8 compute waves split each K block: wave (wn, kq) takes MFMA steps 2 kq and
+// 2 kq + 1 of expert half wn, so every wave keeps one 32 x 32 accumulator; after
+// the last block the four K quarters are added through LDS in kq order (a fixed
+// order; no atomics).
+constexpr int RT3_BM = 32;
+constexpr int RT3_A_BYTES = RT3_BM * BLK * 2;                // 8 KB: 2 lines
+constexpr int RT3_STAGE = RT3_A_BYTES + RT2_BN * BLK * 2;    // + 16 KB: 2 row blocks x 2 lines
+constexpr int RT3_NSTAGE = 5;
+constexpr int RT3_JOBS = RT3_STAGE / 1024 / RT2_PWAVES;      // 6 load instructions per loader wave per block
+constexpr int RT3_RED = 8 * 16 * 64 * 4;                     // 8 waves x 16 values x 64 lanes
+constexpr int RT3_LDS = RT3_NSTAGE * RT3_STAGE + RT3_RED;
+static_assert(RT3_JOBS * RT2_PWAVES * 1024 == RT3_STAGE && RT3_LDS <= 160 * 1024, "stage");
+
+// s_waitcnt vmcnt for n of the loader's blocks still in flight (n <= 3)
+__device__ __forceinline__ void rt3_wait_blocks(int n) {
+  switch (n) {
+    case 3: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
+
+__global__ __launch_bounds__(64 * (RT2_CWAVES + RT2_PWAVES), 1) void router_ksplit_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ g, int T, float* __restrict__ logits) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t rt_lds[];
+  float* red = reinterpret_cast<float*>(rt_lds + RT3_NSTAGE * RT3_STAGE);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int total = (T + RT3_BM - 1) / RT3_BM * RT2_NT;
+  const int first = xcd_remap(blockIdx.x, gridDim.x);
+  int n_items = 0;
+  for (int item = first; item < total; item += gridDim.x) ++n_items;
+  const int G = n_items * NB_H;
+
+  if (wave >= RT2_CWAVES) {
+    // loader wave p: jobs 6 p .. 6 p + 5 of the 24 per block (0-7 hidden rows,
+    // 8-23 gate rows); a job moves 8 rows x 128 B (one line of a K block)
+    const int p = wave - RT2_CWAVES, ld_row = lane >> 3;
+    const uint8_t* src[RT3_JOBS];
+    int dst[RT3_JOBS];
+    int item = first - (int)gridDim.x, kb = NB_H, slot = 0;
+    auto next_item = [&]() {
+      item += gridDim.x;
+      const int mt = item / RT2_NT, nt = item % RT2_NT;
+#pragma unroll
+      for (int i = 0; i < RT3_JOBS; ++i) {
+        const int job = p * RT3_JOBS + i;
+        const int chunk_row = ld_row;
+        if (job < 8) {
+          const int rg = job & 3, h = job >> 2;
+          const int row = min(mt * RT3_BM + rg * 8 + ld_row, T - 1);
+          src[i] = reinterpret_cast<const uint8_t*>(x + (size_t)row * H) + h * 128 +
+                   ((lane & 7) ^ chunk_row ^ (rg & 1)) * 16;
+          dst[i] = h * RT2_REG + rg * 1024;
+        } else {
+          const int jj = job - 8, rg = jj & 3, h = (jj >> 2) & 1, jb = jj >> 3;
+          const int e = nt * RT2_BN + jb * 32 + rg * 8 + ld_row;
+          src[i] = reinterpret_cast<const uint8_t*>(g + (size_t)e * H) + h * 128 +
+                   ((lane & 7) ^ chunk_row ^ (rg & 1)) * 16;
+          dst[i] = RT3_A_BYTES + (jb * 2 + h) * RT2_REG + rg * 1024;
+        }
+      }
+      kb = 0;
+    };
+    auto issue = [&]() {
+      if (kb == NB_H) next_item();
+      uint8_t* st = rt_lds + slot * RT3_STAGE;
+#pragma unroll
+      for (int i = 0; i < RT3_JOBS; ++i) lds_direct16(src[i] + kb * 2 * BLK, st + dst[i]);  // 256 B per K block
+      slot = slot == RT3_NSTAGE - 1 ? 0 : slot + 1;
+      ++kb;
+    };
+    for (int b = 0; b < RT3_NSTAGE - 1 && b < G; ++b) issue();
+#pragma unroll 1
+    for (int gi = 0; gi < G; ++gi) {
+      rt3_wait_blocks(min(RT3_NSTAGE - 2, G - 1 - gi));  // block gi is in
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (gi + RT3_NSTAGE - 1 < G) issue();
+      if (gi % NB_H == NB_H - 1) __builtin_amdgcn_s_barrier();  // the compute waves' K-quarter sum
+    }
+    return;
+  }
+
+  // compute wave (wn, kq): experts 32 wn .. of the item, MFMA steps 2 kq, 2 kq + 1
+  // of every K block; step t reads, from line t / 4 of the row, 16 B chunk
+  // 4 ((t / 2) % 2) + 2 lg + t % 2 (the same for both operands)
+  const int wn = wave & 1, kq = wave >> 1;
+  const int lr = lane & 31, lg = lane >> 5;
+  int off[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) off[tt] = sw32(lr, 4 * (kq & 1) + 2 * lg + tt);
+  const int line = kq >> 1;
+  int slot = 0;
+  for (int item = first; item < total; item += gridDim.x) {
+    const int mt = item / RT2_NT, nt = item % RT2_NT;
+    v16f acc = v16f{};
+#pragma unroll 1
+    for (int kb = 0; kb < NB_H; ++kb) {
+      __builtin_amdgcn_s_barrier();  // block kb is in its slot; the slot before it is free
+      asm volatile("" ::: "memory");
+      const uint8_t* st = rt_lds + slot * RT3_STAGE;
+      slot = slot == RT3_NSTAGE - 1 ? 0 : slot + 1;
+      const uint8_t* sa = st + line * RT2_REG;
+      const uint8_t* sb = st + RT3_A_BYTES + (wn * 2 + line) * RT2_REG;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const v8bf a = *reinterpret_cast<const v8bf*>(sa + off[tt]);
+        const v8bf b = *reinterpret_cast<const v8bf*>(sb + off[tt]);
+        acc = mfma_bf16_32x32x16(a, b, acc);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
+    }
+    // the K quarters: wave w's 16 values per lane to LDS, then wave w takes expert
+    // half w % 2, values 4 (w / 2) .. + 3, and adds the quarters in kq order
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * 64 + lane] = acc[i];
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = 4 * kq + ii;  // this wave's value index (kq doubles as the value group)
+      float v = red[((0 * 2 + wn) * 16 + i) * 64 + lane];
+#pragma unroll
+      for (int q = 1; q < 4; ++q) v += red[((q * 2 + wn) * 16 + i) * 64 + lane];
+      const int t = mt * RT3_BM + 8 * (i >> 2) + 4 * lg + (i & 3);
+      if (t < T) logits[(size_t)t * E_GLOBAL + nt * RT2_BN + wn * 32 + lr] = v;
+    }
+  }
+}
+
 hipError_t launch_quantize_1x128(const uint16_t* x, int T, uint8_t* q, float* scale, hipStream_t stream);
 
 static hipError_t launch_router_tiled(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
@@ -239,10 +381,33 @@ static hipError_t launch_router_tiled(const uint16_t* x, const uint16_t* g, int 
   return hipGetLastError();
 }
 
+static hipError_t launch_router_ksplit(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
+                                       hipStream_t stream) {
+  static PerDeviceOnce<hipError_t> once;
+  hipError_t e = hipErrorInvalidDevice;
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(router_ksplit_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, RT3_LDS); },
+           e);
+  if (e != hipSuccess) return e;
+  const int items = (T + RT3_BM - 1) / RT3_BM * RT2_NT;
+  const int grid = min((items + 7) / 8 * 8, (cu + 7) / 8 * 8);
+  hipLaunchKernelGGL(router_ksplit_kernel, dim3(grid), dim3(64 * (RT2_CWAVES + RT2_PWAVES)), RT3_LDS, stream, x, g,
+                     T, logits);
+  return hipGetLastError();
+}
+
+// the tiled GEMM by token count: 32-token items with the K steps split over the
+// waves while they fit on the CUs in one round, 128-token items beyond
+static hipError_t launch_router_gemm(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
+                                     hipStream_t stream) {
+  return (T + RT3_BM - 1) / RT3_BM * RT2_NT <= cu ? launch_router_ksplit(x, g, T, logits, cu, stream)
+                                                  : launch_router_tiled(x, g, T, logits, cu, stream);
+}
+
 hipError_t launch_router_logits(const uint16_t* x, const uint16_t* g, int T, float* logits, int cu,
                                 hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  if (T >= RT2_MIN_T) return launch_router_tiled(x, g, T, logits, cu, stream);
+  if (T >= RT2_MIN_T) return launch_router_gemm(x, g, T, logits, cu, stream);
   hipLaunchKernelGGL(router_small_kernel<false>, dim3((T + RT_M - 1) / RT_M, E_GLOBAL / 16), dim3(64 * RS_WAVES), 0,
                      stream, x, g, T, logits, nullptr, nullptr);
   return hipGetLastError();
@@ -252,7 +417,7 @@ hipError_t launch_router_quantize(const uint16_t* x, const uint16_t* g, int T, f
                                   int cu, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (T >= RT2_MIN_T) {
-    const hipError_t e = launch_router_tiled(x, g, T, logits, cu, stream);
+    const hipError_t e = launch_router_gemm(x, g, T, logits, cu, stream);
     return e != hipSuccess ? e : launch_quantize_1x128(x, T, q, qs, stream);
   }
   hipLaunchKernelGGL(router_small_kernel<true>, dim3((T + RT_M - 1) / RT_M, E_GLOBAL / 16), dim3(64 * RS_WAVES), 0,

@@ -24,9 +24,11 @@ def gate(dev):
     return g, g.to(dev)
 
 
-# token counts on both kernels (16-token tiles below 576 tokens, 128 x 64 tiles from
-# 576 on) with ragged last tiles and the sizes either side of the switch
-@pytest.mark.parametrize("T", [1, 5, 16, 17, 64, 100, 575, 576, 1024, 3000])
+# token counts on the three kernels (16-token tiles below 576 tokens, 32 x 64 tiles
+# with the K steps split over the waves from 576 while they fit on the CUs, 2,048
+# tokens on 256 CUs, 128 x 64 tiles beyond) with ragged last tiles and the sizes
+# either side of each switch
+@pytest.mark.parametrize("T", [1, 5, 16, 17, 64, 100, 575, 576, 1024, 2047, 2048, 2049, 3000, 4100])
 def test_router_matches_float64(dev, gate, T):
     print(f"router T={T}", flush=True)
     x = wl.hidden_bf16(T, 900 + T)
@@ -50,7 +52,7 @@ def test_router_closed_forms(dev, gate):
     idx = (torch.arange(256) * 28 + 5) % 7168
     gu = torch.zeros((256, 7168), dtype=torch.bfloat16)
     gu[torch.arange(256), idx] = 1.0
-    for T in (3, 40, 700):
+    for T in (3, 40, 700, 3100):
         x = wl.hidden_bf16(T, 12)
         assert torch.equal(fm.router_logits(x.to(dev), gu.to(dev)).cpu(), x.float()[:, idx]), T
 
