@@ -21,6 +21,7 @@ MOE_ERR_ARG = -6
 MOE_ERR_NOALLOC_SIZE = -7
 MOE_FP8_NOALLOC_MAX_TOKENS = 64
 MOE_FP8_MAX_TOKENS = 1 << 17
+MOE_FP8_CHUNK_TOKENS = 1 << 14
 MOE_FP8_HEADER_WORDS = 128
 
 MOE_SHAPE_AUTO = 0

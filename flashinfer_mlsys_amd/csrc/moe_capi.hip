@@ -66,7 +66,7 @@ extern "C" {
 
 size_t moe_fp8_workspace_size(int64_t T) {
   if (T < 0 || T > MOE_FP8_MAX_TOKENS) return 0;
-  return moe::WorkspaceLayout::make(T).total;
+  return moe::WorkspaceLayout::make(T < MOE_FP8_CHUNK_TOKENS ? T : MOE_FP8_CHUNK_TOKENS).total;
 }
 
 }  // extern "C"
@@ -83,6 +83,7 @@ struct Call {
   const uint8_t* w2;
   const float* s2;
   int T;
+  int hs_stride;  // row stride of hidden_states_scale [56, T_call]: T, or the whole call's T for a chunk
   int offset;
   float rsf;
   uint16_t* out;
@@ -111,7 +112,9 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
       !aligned16(gemm2_weights) || !aligned16(gemm2_weights_scale) || !aligned16(output) || !aligned16(workspace))
     return MOE_ERR_ALIGN;
   const bool decode = shape == MOE_SHAPE_AUTO && T <= kDecodeMaxTokens;
-  const WorkspaceLayout L = WorkspaceLayout::make(T, !decode);  // the decode kernels use no partial rows
+  // calls above MOE_FP8_CHUNK_TOKENS run chunk by chunk in one chunk's workspace
+  const int64_t Tw = T < MOE_FP8_CHUNK_TOKENS ? T : MOE_FP8_CHUNK_TOKENS;
+  const WorkspaceLayout L = WorkspaceLayout::make(Tw, !decode);  // the decode kernels use no partial rows
   if (workspace_bytes < L.total) return MOE_ERR_WORKSPACE;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   c.logits = routing_logits;
@@ -123,6 +126,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   c.w2 = gemm2_weights;
   c.s2 = gemm2_weights_scale;
   c.T = (int)T;
+  c.hs_stride = (int)T;
   c.offset = clamp_offset(local_expert_offset);
   c.rsf = (float)routed_scaling_factor;
   c.out = output;
@@ -166,7 +170,7 @@ hipError_t run_stage(int stage, const Call& c) {
                                    c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr, c.perm_tok, c.perm_w,
                                    c.tok_pair, c.c_act, grid, c.stream);
       }
-      return launch_gemm1_prefill(c.hidden, c.hscale, c.T, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
+      return launch_gemm1_prefill(c.hidden, c.hscale, c.hs_stride, c.w13, c.s13, c.hdr, c.perm_tok, c.c_act,
                                  (cu_count() + 7) / 8 * 8, c.stream);
     case 2:
       if (c.decode) return launch_gemm2_decode(c.c_act, c.w2, c.s2, c.hdr, c.perm_tok, c.perm_w, c.T, c.out, c.stream);
@@ -194,9 +198,23 @@ static int forward(int shape, const float* routing_logits, const uint16_t* routi
                            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,
                            routed_scaling_factor, output, workspace, workspace_bytes, stream, shape, c);
   if (v <= 0) return v;
-  for (int stage = 0; stage < 4; ++stage) {
-    const hipError_t e = run_stage(stage, c);
-    if (e != hipSuccess) return hip_fail(e);
+  // Tokens are independent (routing, experts and the sum over a token's experts
+  // are all per token), so a call above MOE_FP8_CHUNK_TOKENS runs as consecutive
+  // calls over token chunks, each with the chunk's rows of every per-token input
+  // and output; only hidden_states_scale [56, T] keeps the whole call's row
+  // stride. Every chunk's result is bit for bit the one a separate call gives.
+  const int T_all = c.T;
+  for (int t0 = 0; t0 < T_all; t0 += MOE_FP8_CHUNK_TOKENS) {
+    Call k = c;
+    k.T = T_all - t0 < MOE_FP8_CHUNK_TOKENS ? T_all - t0 : MOE_FP8_CHUNK_TOKENS;
+    k.logits = c.logits + (size_t)t0 * moe::E_GLOBAL;
+    k.hidden = c.hidden + (size_t)t0 * moe::H;
+    k.hscale = c.hscale + t0;
+    k.out = c.out + (size_t)t0 * moe::H;
+    for (int stage = 0; stage < 4; ++stage) {
+      const hipError_t e = run_stage(stage, k);
+      if (e != hipSuccess) return hip_fail(e);
+    }
   }
   return MOE_OK;
 }
@@ -230,6 +248,7 @@ int moe_fp8_run_stage(int stage, int shape, const float* routing_logits, const u
                       double routed_scaling_factor, uint16_t* output, void* workspace, size_t workspace_bytes,
                       void* stream) {
   if (stage < 0 || stage > 3) return MOE_ERR_ARG;
+  if (T > MOE_FP8_CHUNK_TOKENS) return MOE_ERR_SIZE;  // a stage spans the whole call, which is one chunk at most
   Call c;
   const int v = check_call(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                            gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, T, local_expert_offset,

@@ -142,6 +142,17 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_scatter_kernel(
   __shared__ unsigned long long wmask[DISPATCH_WAVES][E_LOCAL];  // per wave and expert: lanes whose token selected it
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nchunks = gridDim.x, chunk = blockIdx.x;
+  // this chunk's tokens (which local experts each selected, in which slot) and
+  // their weights are requested first, so that their latency overlaps the chunk
+  // counts' below
+  const int t = chunk * DISPATCH_CHUNK + tid;
+  int slot_of[TOP_K];
+  const uint32_t mask = local_mask(topk_ids, t, T, offset, slot_of);
+  float4 w8[2] = {float4{0.f, 0.f, 0.f, 0.f}, float4{0.f, 0.f, 0.f, 0.f}};
+  if (t < T) {
+    w8[0] = reinterpret_cast<const float4*>(topk_w + (size_t)t * TOP_K)[0];
+    w8[1] = reinterpret_cast<const float4*>(topk_w + (size_t)t * TOP_K)[1];
+  }
   {
     const int e = tid & (E_LOCAL - 1), part = tid / E_LOCAL;
     int all = 0, before = 0;
@@ -152,6 +163,10 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_scatter_kernel(
     }
     part_all[part][e] = all;
     part_pre[part][e] = before;
+  }
+  for (int e = 0; e < E_LOCAL; ++e) {  // uniform over the wave
+    const unsigned long long m = __ballot((mask >> e) & 1u);
+    if (lane == 0) wmask[wave][e] = m;
   }
   __syncthreads();
   if (tid < E_LOCAL) {  // lanes 0-31 of wave 0: one expert each
@@ -180,17 +195,10 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_scatter_kernel(
       if (tid >= nact) hdr->active[tid] = -1;
     }
   }
-  // this chunk's tokens: which local experts each selected, and in which slot
-  const int t = chunk * DISPATCH_CHUNK + tid;
-  int slot_of[TOP_K];
-  const uint32_t mask = local_mask(topk_ids, t, T, offset, slot_of);
-  for (int e = 0; e < E_LOCAL; ++e) {  // uniform over the wave
-    const unsigned long long m = __ballot((mask >> e) & 1u);
-    if (lane == 0) wmask[wave][e] = m;
-  }
   __syncthreads();
   if (mask) {
     const unsigned long long lt = (1ull << lane) - 1ull;
+    const float wv[TOP_K] = {w8[0].x, w8[0].y, w8[0].z, w8[0].w, w8[1].x, w8[1].y, w8[1].z, w8[1].w};
 #pragma unroll
     for (int j = 0; j < TOP_K; ++j) {
       const int e = slot_of[j];
@@ -199,7 +207,7 @@ __global__ __launch_bounds__(DISPATCH_CHUNK) void dispatch_scatter_kernel(
       for (int w = 0; w < wave; ++w) before += __popcll(wmask[w][e]);
       const int pos = seg[e] + pre[e] + before + __popcll(wmask[wave][e] & lt);
       perm_tok[pos] = t;
-      perm_w[pos] = topk_w[(size_t)t * TOP_K + j];
+      perm_w[pos] = wv[j];
       tok_pair[(size_t)t * TOP_K + j] = pos;
     }
   }

@@ -37,9 +37,15 @@ enum {
  * T <= 64 and the prefill kernels above (AUTO), or the prefill kernels at any T. */
 enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
-/* Largest T any entry point accepts: the worst-case workspace (8 local pairs per
- * token, moe_fp8_workspace_size) is about 262 KB per token, 34 GB at this T. */
+/* Largest T any entry point accepts. */
 #define MOE_FP8_MAX_TOKENS (1 << 17)
+
+/* Forward calls above this many tokens run the operator over consecutive token
+ * chunks of this size (the last one shorter), in one chunk's workspace: the
+ * worst-case workspace (8 local pairs per token, fp32 rows of every pair) is
+ * about 262 KB per token, 4.3 GB for one chunk. Tokens are independent, so the
+ * output is bit for bit the unchunked one. */
+#define MOE_FP8_CHUNK_TOKENS (1 << 14)
 
 /* Words of the `header` buffer moe_fp8_dispatch and moe_fp8_route_dispatch take
  * for T tokens: the dispatch header (MOE_FP8_HEADER_WORDS) followed by 32 counts
@@ -48,7 +54,8 @@ enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 #define MOE_FP8_DISPATCH_HEADER_WORDS(T) (MOE_FP8_HEADER_WORDS + 32 * (((T) + 255) / 256))
 
 /* Bytes of device workspace one forward call needs for T tokens (worst case
- * of 8 routed local pairs per token). */
+ * of 8 routed local pairs per token; for T above MOE_FP8_CHUNK_TOKENS the size
+ * for one chunk). */
 size_t moe_fp8_workspace_size(int64_t T);
 
 /*
@@ -118,7 +125,8 @@ int moe_fp8_forward_shape(int shape, const float* routing_logits, const uint16_t
  * T > 64), 1 = GEMM1 + SwiGLU (+ the in-workgroup dispatch for T <= 64),
  * 2 = GEMM2 x routing weight (+ the ordered combine for T <= 64), 3 = the
  * combine (T > 64; nothing for T <= 64). A stage's inputs must already be in
- * the workspace (a moe_fp8_forward with the same arguments ran on it). No
+ * the workspace (a moe_fp8_forward with the same arguments ran on it); T at most
+ * MOE_FP8_CHUNK_TOKENS (MOE_ERR_SIZE above: the forward would run chunks). No
  * reference counterpart (the reference timed its stages with torch.profiler,
  * scripts/ncu_profile.py:89-143): the benchmark times each kernel over many
  * back-to-back launches of its stage.

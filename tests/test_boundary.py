@@ -46,8 +46,12 @@ def test_abi_version_and_strings(lib):
 def test_workspace_size(lib):
     assert lib.moe_fp8_workspace_size(-1) == 0
     assert lib.moe_fp8_workspace_size(_lib.MOE_FP8_MAX_TOKENS + 1) == 0
-    # the worst case stays allocatable on one 288 GB GPU
-    assert lib.moe_fp8_workspace_size(_lib.MOE_FP8_MAX_TOKENS) < 40e9
+    # calls above the chunk size run chunk by chunk in one chunk's workspace
+    chunk = lib.moe_fp8_workspace_size(_lib.MOE_FP8_CHUNK_TOKENS)
+    assert chunk < 5e9
+    for T in (_lib.MOE_FP8_CHUNK_TOKENS + 1, 20000, _lib.MOE_FP8_MAX_TOKENS):
+        assert lib.moe_fp8_workspace_size(T) == chunk
+    assert lib.moe_fp8_workspace_size(_lib.MOE_FP8_CHUNK_TOKENS - 1) < chunk
     assert lib.moe_fp8_workspace_size(0) > 0
     prev = 0
     for T in (1, 2, 16, 1024, 8192):

@@ -331,6 +331,31 @@ def test_other_offsets_match_oracle(case, offset):
     assert_close_bf16(out, ref, f"offset {offset}")
 
 
+def test_chunked_forward_equals_separate_calls(weights, dev):
+    """A call above MOE_FP8_CHUNK_TOKENS runs chunk by chunk in one chunk's
+    workspace: its output equals, bit for bit, separate calls over the token chunks
+    (each with its own columns of hidden_states_scale, which the chunked call reads
+    with the whole call's row stride), and rows on both sides of the chunk edge
+    match the oracle run on those tokens alone."""
+    from flashinfer_mlsys_amd import _lib
+    C = _lib.MOE_FP8_CHUNK_TOKENS
+    T = C + 1000
+    lg, b, hs, hss = wl.make_activations(T, 4242)
+    offset, rsf = 64, 2.5
+    _say(f"chunked forward T={T}")
+    g = [t.to(dev) for t in (lg, b, hs, hss)]
+    out = fm.run(*g, *weights[1], offset, rsf)
+    parts = []
+    for a, e in ((0, C), (C, T)):
+        parts.append(fm.run(g[0][a:e].contiguous(), g[1], g[2][a:e].contiguous(), g[3][:, a:e].contiguous(),
+                            *weights[1], offset, rsf))
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), torch.cat(parts).view(torch.int16))
+    rows = torch.tensor([0, 1, C - 2, C - 1, C, C + 1, T - 2, T - 1])
+    ref = cpu_ref.run(lg[rows], b, hs[rows], hss[:, rows].contiguous(), *weights[0], offset, rsf).float().numpy()
+    assert_close_bf16(out.float().cpu().numpy()[rows.numpy()], ref, "rows at the chunk edge")
+
+
 def test_zero_tokens(weights, dev):
     w13, s13, w2, s2 = weights[1]
     lg = torch.empty((0, 256), dtype=torch.float32, device=dev)
