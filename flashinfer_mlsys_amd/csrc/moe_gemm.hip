@@ -1244,24 +1244,28 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
   }
   // epilogue: weight by the pair's routing weight, one fp32 row per pair. The
-  // weights of a row block's 16 rows per lane are requested at once (rows past
-  // the valid ones read the last valid row's weight, unused), so its stores wait
-  // for one round trip, not one per row behind the stores before it.
+  // weights of a row block's 32 rows are uniform over the wave and read with
+  // scalar loads (counted by lgkmcnt), so no wait covers the stores before them:
+  // a vector load here would wait, on vmcnt, for every store in flight. Rows past
+  // the valid ones read the next pairs' weights (or the workspace region after
+  // the weights), unused.
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    float w[16];
+    const float* wp = perm_w + it.seg + it.m0 + (2 * i + wm) * 32;  // uniform
+    float wl[16], wh[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
-      w[r] = perm_w[it.seg + min(row, it.cnt - 1)];
+      wl[r] = wp[8 * (r / 4) + (r % 4)];
+      wh[r] = wp[8 * (r / 4) + 4 + (r % 4)];
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
       if (row < it.cnt) {
+        const float w = lg ? wh[r] : wl[r];
         float* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w[r];
+        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
       }
     }
   }
