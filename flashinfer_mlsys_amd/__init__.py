@@ -52,12 +52,22 @@ def _req(cond, msg):
 
 
 def _on_gpu(t, name):
-    _req(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
-    _req(t.is_cuda, f"{name} must be on a ROCm GPU (got {t.device}); there is no CPU path")
+    # (the messages are formatted only on failure: this runs on every call)
+    if not isinstance(t, torch.Tensor):
+        raise MoEInputError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise MoEInputError(f"{name} must be on a ROCm GPU (got {t.device}); there is no CPU path")
     return t
 
 
+# The current stream's raw handle for a device index (the accessor torch's own
+# generated code uses; about a tenth of the cost of current_stream(...).cuda_stream).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device):
+    if _raw_stream is not None:
+        return _raw_stream(device.index if isinstance(device, torch.device) else int(device))
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -83,9 +93,10 @@ def _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, 
           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale]
     for t, n in zip(ts, names):
         _on_gpu(t, n)
-    dev = hidden_states.device
+    dev = hidden_states.get_device()
     for t, n in zip(ts, names):
-        _req(t.device == dev, f"{n} is on {t.device}, expected {dev}")
+        if t.get_device() != dev:
+            raise MoEInputError(f"{n} is on {t.device}, expected {hidden_states.device}")
     _req(routing_logits.dim() == 2, "routing_logits must be [T, 256]")
     T = routing_logits.shape[0]
     _req(routing_logits.shape[1] == E_GLOBAL, "num_experts must be 256")
@@ -104,7 +115,8 @@ def _validate(routing_logits, routing_bias, hidden_states, hidden_states_scale, 
     _req(gemm2_weights.dtype == torch.float8_e4m3fn, "gemm2_weights must be float8_e4m3fn")
     for t, n in ((hidden_states_scale, "hidden_states_scale"), (gemm1_weights_scale, "gemm1_weights_scale"),
                  (gemm2_weights_scale, "gemm2_weights_scale")):
-        _req(t.dtype == torch.float32, f"{n} must be float32")
+        if t.dtype != torch.float32:
+            raise MoEInputError(f"{n} must be float32")
     return T
 
 
@@ -115,7 +127,7 @@ def _forward(shape, routing_logits, routing_bias, hidden_states, hidden_states_s
                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
     _on_gpu(output, "output")
     _req(output.shape == (T, H) and output.dtype == torch.bfloat16, "output must be bf16 [T, 7168]")
-    _req(output.device == hidden_states.device, "output must be on the inputs' device")
+    _req(output.get_device() == hidden_states.get_device(), "output must be on the inputs' device")
     if T == 0:
         return None
     lib = _lib.load()
@@ -127,13 +139,18 @@ def _forward(shape, routing_logits, routing_bias, hidden_states, hidden_states_s
                                  gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)]
     out = output if (output.is_contiguous() and output.data_ptr() % 16 == 0) else torch.empty_like(
         output, memory_format=torch.contiguous_format)
-    with torch.cuda.device(hidden_states.device):
+    def call():
         tail = (T, int(local_expert_offset), float(routed_scaling_factor), out.data_ptr(), workspace.data_ptr(),
                 workspace.numel() * workspace.element_size(), _stream(hidden_states.device))
         if shape == SHAPE_AUTO:
-            code = lib.moe_fp8_forward(*[a.data_ptr() for a in args], *tail)
-        else:
-            code = lib.moe_fp8_forward_shape(int(shape), *[a.data_ptr() for a in args], *tail)
+            return lib.moe_fp8_forward(*[a.data_ptr() for a in args], *tail)
+        return lib.moe_fp8_forward_shape(int(shape), *[a.data_ptr() for a in args], *tail)
+
+    if torch.cuda.current_device() == hidden_states.get_device():
+        code = call()
+    else:  # the library launches on the current device
+        with torch.cuda.device(hidden_states.device):
+            code = call()
     _lib.check(code, "moe_fp8_forward")
     if out is not output:
         output.copy_(out)
