@@ -1421,7 +1421,9 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
 
 // ---------------------------------------------------------------------------
 // Ordered combine: out[t] = bf16( sum_j partial[pair(t, j)] ) over t's local
-// experts in ascending id; zeros for tokens with none.
+// experts in ascending id; zeros for tokens with none. The fp32 pair rows are
+// read once: non-temporal loads, which leave the caches (the 256 MB memory-side
+// cache above all) to data that is used again, such as the expert weights.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
                                                       const int32_t* __restrict__ tok_pair, int T,
@@ -1431,15 +1433,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   int p[TOP_K];
 #pragma unroll
   for (int j = 0; j < TOP_K; ++j) p[j] = tok_pair[(size_t)t * TOP_K + j];
-  float4 v[TOP_K];
+  v4f v[TOP_K];
 #pragma unroll
-  for (int j = 0; j < TOP_K; ++j)
-    v[j] = p[j] >= 0 ? *reinterpret_cast<const float4*>(partial + (size_t)p[j] * H + h) : float4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < TOP_K; ++j) {
+    v[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (p[j] >= 0) v[j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(partial + (size_t)p[j] * H + h));
+  }
   float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < TOP_K; ++j)  // ascending slot = ascending expert id
     if (p[j] >= 0) {
-      acc.x += v[j].x; acc.y += v[j].y; acc.z += v[j].z; acc.w += v[j].w;
+      acc.x += v[j][0]; acc.y += v[j][1]; acc.z += v[j][2]; acc.w += v[j][3];
     }
   uint2 o;
   o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
