@@ -220,7 +220,8 @@ def cpu_baseline(sweep_names):
 
 def cpu_oracle_us(name):
     """One timed call of the oracle on the host CPU for a configuration (the reference's own
-    per-workload CPU figure; BASELINE's path 2: one call for T >= 1024)."""
+    per-workload CPU figure, presentation/data.py:4-24; a single call, as one call
+    already takes seconds at these sizes)."""
     from oracle import cpu_ref  # only the CPU-baseline leg uses the oracle
     w = wl.WORKLOADS[name]
     w13, s13, w2, s2 = wl.make_weights()
