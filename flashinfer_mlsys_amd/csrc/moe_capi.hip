@@ -358,7 +358,7 @@ int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_we
 namespace {
 
 constexpr size_t kNoAllocScratchBytes = moe::WorkspaceLayout::make(MOE_FP8_NOALLOC_MAX_TOKENS, false).total;
-static_assert(kNoAllocScratchBytes < (4u << 20), "a modest scratch: header, ids, permutation and bf16 C rows");
+static_assert(kNoAllocScratchBytes < (4u << 20), "a modest scratch: header, ids, permutation and fp16 C rows");
 
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
