@@ -23,7 +23,11 @@ Printed JSON line (rank 0, one line):
   also          the other benchmark configurations (prefill 1024 / 8192, skew 4096, and the two
                 largest official token counts 11,948 / 14,107 with their bias profile), each with
                 a roofline object against its binding roof (HBM bytes / 8 TB/s or e4m3 GEMM1 at
-                5.0 PFLOP/s + fp16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; the drop-in
+                5.0 PFLOP/s + fp16 GEMM2 at 2.5 PFLOP/s) and its CPU-oracle time; `official`: the
+                19 official trace workloads (T, offset) in the notebook's order, one row each
+                (us/call, binding roofline, P, E_act, CPU-oracle time); every configuration's
+                error over its whole output against the oracle's output (max abs, max rel, worst
+                err / (atol + rtol |ref|)); the drop-in
                 Python entry point timed at T=1 (host cost included); and the producer-side
                 kernels (FP8 activation quantiser, router GEMM, both fused) at T = 64 and 8192
 """
@@ -68,8 +72,9 @@ class Case:
     """One workload's device inputs plus its routing statistics (P, E_act)."""
 
     def __init__(self, name, dev, weights_gpu):
-        w = wl.WORKLOADS[name]
-        self.name, self.T, self.offset, self.rsf = name, w.T, w.local_expert_offset, w.routed_scaling_factor
+        w = wl.WORKLOADS[name] if isinstance(name, str) else name
+        self.workload = w
+        self.name, self.T, self.offset, self.rsf = w.name, w.T, w.local_expert_offset, w.routed_scaling_factor
         acts = wl.workload_activations(w)
         self.args = [a.to(dev) for a in acts] + list(weights_gpu)
         self.out = torch.empty((w.T, wl.H), dtype=torch.bfloat16, device=dev)
@@ -190,7 +195,22 @@ def check_against_golden(c: Case):
             "max_err_over_bar": round(float(ratio.max()), 4)}
 
 
-def cpu_baseline(sweep_names):
+def whole_output_error(got_bf16, ref_bf16):
+    """Error of the GPU output over the whole [T, 7168] output against the oracle's (both bf16,
+    on the host), as the reference's runner records per workload (scripts/run_local.py:71-73):
+    max |got - ref|, max |got - ref| / |ref| over the elements with ref != 0, and the worst
+    |got - ref| / (atol + rtol |ref|) for atol = 1e-2, rtol = 2e-2 (within the bar when <= 1)."""
+    g = got_bf16.float().double()
+    r = ref_bf16.float().double()
+    d = (g - r).abs()
+    nz = r != 0
+    rel = float((d[nz] / r[nz].abs()).max()) if bool(nz.any()) else 0.0
+    return {"elements": int(d.numel()), "max_abs_error": float(d.max()) if d.numel() else 0.0,
+            "max_rel_error": rel,
+            "max_err_over_bar": round(float((d / (1e-2 + 2e-2 * r.abs())).max()), 4) if d.numel() else 0.0}
+
+
+def cpu_baseline(sweep_names, outputs=None):
     """The oracle on the host CPU over one call per T of the sweep."""
     from oracle import cpu_ref  # only the CPU-baseline leg uses the oracle
     threads = torch.get_num_threads()
@@ -200,9 +220,12 @@ def cpu_baseline(sweep_names):
         w = wl.WORKLOADS[name]
         acts = wl.workload_activations(w)
         t0 = time.perf_counter()
-        cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor, materialize_all=True)
+        ref = cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor,
+                          materialize_all=True)
         tot_t += time.perf_counter() - t0
         tot_tok += w.T
+        if outputs is not None:
+            outputs[name] = ref
     return {
         "value": round(tot_tok / tot_t, 4),
         "unit": "tokens/s",
@@ -221,14 +244,15 @@ def cpu_baseline(sweep_names):
 def cpu_oracle_us(name):
     """One timed call of the oracle on the host CPU for a configuration (the reference's own
     per-workload CPU figure, presentation/data.py:4-24; a single call, as one call
-    already takes seconds at these sizes)."""
+    already takes seconds at these sizes): (us, the oracle's bf16 output)."""
     from oracle import cpu_ref  # only the CPU-baseline leg uses the oracle
-    w = wl.WORKLOADS[name]
+    w = wl.WORKLOADS[name] if isinstance(name, str) else name
     w13, s13, w2, s2 = wl.make_weights()
     acts = wl.workload_activations(w)
     t0 = time.perf_counter()
-    cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor, materialize_all=True)
-    return (time.perf_counter() - t0) * 1e6
+    ref = cpu_ref.run(*acts, w13, s13, w2, s2, w.local_expert_offset, w.routed_scaling_factor,
+                      materialize_all=True)
+    return (time.perf_counter() - t0) * 1e6, ref
 
 
 def binding_roofline(c, us):
@@ -341,14 +365,18 @@ def main():
         return
     extra = [] if args.no_extra else ["t16", "prefill_t1024", "prefill_t8192", "skew_t4096", "trace_t11948",
                                       "trace_t14107"]
+    # the official trace workloads other than the two largest (those are trace_t11948 / trace_t14107)
+    official = [] if args.no_extra else [wl.official_workload(*o) for o in wl.OFFICIAL_TRACE if o[1] < 4096]
     cases = {n: Case(n, dev, weights_gpu) for n in sweep + extra}
+    cases.update({w.name: Case(w, dev, weights_gpu) for w in official})
     runner = Runner(dev, max(c.T for c in cases.values()))
 
-    accuracy = {}
+    accuracy, gpu_out = {}, {}
     for c in cases.values():
         runner.call(c)
         torch.cuda.synchronize()
         accuracy[c.name] = check_against_golden(c)
+        gpu_out[c.name] = c.out.cpu()  # compared in full with the oracle's output in the CPU leg
         for stage in range(4):  # the per-stage path must reproduce the forward's output
             runner.stage(c, stage)
         torch.cuda.synchronize()
@@ -466,6 +494,25 @@ def main():
     for row, c in zip(per_T, sweep_cases):
         row["roofline"] = binding_roofline(c, row["us_per_call"])
 
+    # the 19 official workloads (input_analysis/input_check.ipynb cell 7), one row each, in the
+    # notebook's order, as the reference's per-workload table (notes/solution_benchmarks.md:158-176)
+    if official:
+        big = {(cases[n].T, cases[n].offset): n for n in ("trace_t11948", "trace_t14107")}
+        rows = []
+        for uuid, T, off in wl.OFFICIAL_TRACE:
+            n = big.get((T, off)) or wl.official_workload(uuid, T, off).name
+            c = cases[n]
+            if n in also:
+                us = also[n]["us_per_call"]
+            else:
+                us, _ = runner.harness_us(lambda: runner.call(c))
+            rows.append({"uuid": uuid, "T": T, "local_expert_offset": off, "P": c.P, "E_act": c.E_act,
+                         "us_per_call": round(us, 2), "tokens_per_s": round(T / (us * 1e-6), 1),
+                         "roofline": binding_roofline(c, us), "workload": n})
+            log(f"official T={T} offset={off}: {us:.1f} us/call, P={c.P}, E_act={c.E_act}, "
+                f"{rows[-1]['roofline']['frac']} of the {rows[-1]['roofline']['bound']} roof")
+        also["official"] = rows
+
     # the drop-in Python entry point at T=1: validation, workspace from torch's allocator and
     # the ctypes call included (host wall clock per call over back-to-back calls)
     c1 = cases["decode_t1"]
@@ -541,12 +588,31 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
-        cpu = cpu_baseline(sweep)
+        ref_out = {}
+        cpu = cpu_baseline(sweep, ref_out)
+        for row, c in zip(per_T, sweep_cases):
+            row["error_vs_oracle_full_output"] = whole_output_error(gpu_out[c.name], ref_out[c.name])
         for n in extra:  # one timed oracle call per other configuration
-            us = cpu_oracle_us(n)
+            us, ref = cpu_oracle_us(n)
             also[n]["cpu_oracle_us_per_call"] = round(us, 1)
             also[n]["gpu_speedup_vs_cpu_oracle"] = round(us / also[n]["us_per_call"], 1)
-            log(f"CPU oracle {n}: {us / 1e6:.2f} s")
+            also[n]["error_vs_oracle_full_output"] = whole_output_error(gpu_out[n], ref)
+            log(f"CPU oracle {n}: {us / 1e6:.2f} s, worst err/bar over the whole output "
+                f"{also[n]['error_vs_oracle_full_output']['max_err_over_bar']}")
+        for row in also.get("official", []):
+            n = row["workload"]
+            if n in also:
+                row["cpu_oracle_us_per_call"] = also[n]["cpu_oracle_us_per_call"]
+                row["error_vs_oracle_full_output"] = also[n]["error_vs_oracle_full_output"]
+            else:
+                us, ref = cpu_oracle_us(cases[n].workload)
+                row["cpu_oracle_us_per_call"] = round(us, 1)
+                row["error_vs_oracle_full_output"] = whole_output_error(gpu_out[n], ref)
+            row["gpu_speedup_vs_cpu_oracle"] = round(row["cpu_oracle_us_per_call"] / row["us_per_call"], 1)
+        if also.get("official"):
+            log("official workloads: worst err/bar over the whole output "
+                + ", ".join(f"T={r['T']} {r['error_vs_oracle_full_output']['max_err_over_bar']}"
+                            for r in also["official"]))
 
     out = {
         "metric": METRIC,

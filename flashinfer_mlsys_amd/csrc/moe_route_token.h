@@ -172,24 +172,30 @@ __device__ __forceinline__ void route_token_exact(const float* __restrict__ logi
 #pragma unroll
   for (int i = 0; i < 4; ++i) sel[i] = (selmask >> i) & 1u;
   const unsigned long long lt = (1ull << lane) - 1ull;
-  int pos = 0;
-  float ssum = 0.f;
+  int pos0 = 0;  // selected experts of the lanes below: this lane's first position
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    pos += __popcll(__ballot(sel[i]) & lt);
-    ssum += sel[i] ? s[i] : 0.f;
+  for (int i = 0; i < 4; ++i) pos0 += __popcll(__ballot(sel[i]) & lt);
+  // the denominator: the 8 selected s gathered in ascending id order (through the
+  // scratch), summed by the tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7))
+  // in every 8-lane slice, the same sum as the fast path's, so a token's weights
+  // do not depend on which path routed it
+  VTie& sc = lds_tie(tie);
+  {
+    int pos = pos0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (sel[i]) {
+        sc.key[pos] = __float_as_uint(s[i]);
+        ++pos;
+      }
+    }
   }
-  // sum over the wave: within each row of 16 (every lane of the row ends with the
-  // same value), then the four row sums in row order
+  float ssum = __uint_as_float(sc.key[lane & (TOP_K - 1)]);
   ssum += dpp_f<DPP_XOR1>(ssum);
   ssum += dpp_f<DPP_XOR2>(ssum);
   ssum += dpp_f<DPP_HALF_MIRROR>(ssum);
-  ssum += dpp_f<DPP_MIRROR>(ssum);
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 48));
-  const float denom = ((r0 + r1) + (r2 + r3)) + 1e-20f;
+  const float denom = ssum + 1e-20f;
+  int pos = pos0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (sel[i]) {
@@ -368,7 +374,9 @@ __device__ __forceinline__ bool route_token_fast(const float* __restrict__ logit
   const float xj = __uint_as_float(sc.key[j]);
   const int idj = (int)sc.id[j];
   const float sj = exact_sigmoid(xj);
-  float ssum = sj;  // lanes 0-7: the 8-lane sum (each 8-lane slice holds the same 8 values)
+  // the 8-lane tree ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) (each 8-lane
+  // slice holds the same 8 values), as the exact path sums them
+  float ssum = sj;
   ssum += dpp_f<DPP_XOR1>(ssum);
   ssum += dpp_f<DPP_XOR2>(ssum);
   ssum += dpp_f<DPP_HALF_MIRROR>(ssum);

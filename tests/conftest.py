@@ -80,22 +80,22 @@ def weights(dev):
 
 
 # --- Trace-replay cases -----------------------------------------------------
+from flashinfer_mlsys_amd import workloads as wl  # noqa: E402
+
 # Token counts and local-expert offsets of the official FlashInfer-Trace
 # workloads for this operator (input_analysis/input_check.ipynb cell 7: T from
 # 1 to 14107, offsets 0..224), with their routing-bias profile (every bias
 # 4.9375 or 4.96875, two adjacent bf16 values, cell 5). The uuids are the first
 # of "mi355x-trace-<T>-<offset>-<k>" whose routing has at least one local pair
 # and selection margins of at least 8 fp32 ulps (test_trace checks both).
-TRACE_CASES = [
-    ("mi355x-trace-7-192-0", 7, 192),
-    ("mi355x-trace-1-32-1", 1, 32),
-    ("mi355x-trace-80-96-0", 80, 96),
-    ("mi355x-trace-901-96-1", 901, 96),
-    ("mi355x-trace-16-224-0", 16, 224),
-    ("mi355x-trace-62-96-0", 62, 96),
-    ("mi355x-trace-14-0-0", 14, 0),
-    ("mi355x-trace-32-32-0", 32, 32),
-]
+# Together with the two largest (T = 11,948 at offset 128 and T = 14,107 at
+# offset 32, the workloads trace_t11948 / trace_t14107) these are all 19 official
+# (T, offset) pairs, in the notebook's order.
+TRACE_CASES = [c for c in wl.OFFICIAL_TRACE if c[1] < 4096]
+# The official (T, offset) pairs (input_analysis/input_check.ipynb cell 7).
+OFFICIAL_PAIRS = [(7, 192), (1, 32), (32, 32), (80, 96), (901, 96), (16, 224), (15, 32), (14, 0), (14107, 32),
+                  (11948, 128), (62, 96), (59, 160), (58, 64), (57, 96), (56, 64), (55, 128), (54, 128),
+                  (53, 32), (52, 160)]
 
 
 def trace_case_tensors(uuid, T):

@@ -151,6 +151,20 @@ def test_route_fast_path_certification(dev, T, bias_kind):
                                rtol=4e-7 * 8, atol=0)
 
 
+def test_route_weights_do_not_depend_on_the_path(dev):
+    """A token's routing weights are the same bits whether the fast path (calls of
+    6,144 tokens or more) or the exact path (smaller calls) routed it: both sum the 8
+    selected scores, in ascending id order, by the same tree. The first 300 rows of a
+    6,144-token call are routed again as a call of their own."""
+    rng = np.random.default_rng(6144)
+    lg = torch.from_numpy(rng.standard_normal((6144, 256), dtype=np.float32)).to(dev)
+    bias = torch.from_numpy((rng.standard_normal(256) * 0.1).astype(np.float32)).to(torch.bfloat16).to(dev)
+    ids_big, w_big, _ = fm.route(lg, bias, 2.5)
+    ids_small, w_small, _ = fm.route(lg[:300].contiguous(), bias, 2.5)
+    assert torch.equal(ids_big[:300], ids_small)
+    assert torch.equal(w_big[:300].view(torch.int32), w_small.view(torch.int32))
+
+
 @pytest.mark.parametrize("case", ALL, indirect=True)
 def test_route_selection_bit_exact(case):
     ids, w, _ = fm.route(case.gpu[0], case.gpu[1], case.rsf)

@@ -201,3 +201,14 @@ def test_trace_cases_are_well_posed():
         assert int(((ids >= offset) & (ids < offset + 32)).sum()) > 0, uuid
         vals = np.unique(b.float().numpy())
         assert set(vals.tolist()) <= {4.9375, 4.96875}
+
+
+def test_trace_cases_cover_every_official_workload():
+    """The trace cases plus the two largest official workloads (trace_t11948,
+    trace_t14107) are exactly the 19 official (T, offset) pairs."""
+    from conftest import OFFICIAL_PAIRS
+    pairs = [(T, off) for _, T, off in TRACE_CASES]
+    pairs += [(wl.WORKLOADS[n].T, wl.WORKLOADS[n].local_expert_offset) for n in ("trace_t11948", "trace_t14107")]
+    assert len(OFFICIAL_PAIRS) == 19 and sorted(pairs) == sorted(OFFICIAL_PAIRS)
+    for uuid, T, off in TRACE_CASES:
+        assert uuid.startswith(f"mi355x-trace-{T}-{off}-")
