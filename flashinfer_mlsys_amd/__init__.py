@@ -76,8 +76,8 @@ def _contig(t):
 
 
 def _header_words(T: int) -> int:
-    """MOE_FP8_DISPATCH_HEADER_WORDS(T): the header, then 32 counts per 256-token chunk."""
-    return _lib.MOE_FP8_HEADER_WORDS + 32 * ((T + 255) // 256)
+    """MOE_FP8_DISPATCH_HEADER_WORDS(T): the header, then 32 counts per group of 16 tokens."""
+    return _lib.MOE_FP8_HEADER_WORDS + 32 * ((T + 15) // 16)
 
 
 def workspace_size(T: int) -> int:
@@ -336,8 +336,9 @@ def dispatch(topk_ids, topk_w, tok_pair, local_expert_offset):
     with torch.cuda.device(dev):
         code = _lib.load().moe_fp8_dispatch(topk_ids.data_ptr() if T else None,
                                             topk_w.data_ptr() if T else None, T, int(local_expert_offset),
-                                            header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
-                                            tok_pair.data_ptr() if T else header.data_ptr(), _stream(dev))
+                                            header.data_ptr(), header.numel(), perm_tok.data_ptr(),
+                                            perm_w.data_ptr(), tok_pair.data_ptr() if T else header.data_ptr(),
+                                            _stream(dev))
     _lib.check(code, "moe_fp8_dispatch")
     return header[:_lib.MOE_FP8_HEADER_WORDS], perm_tok, perm_w, tok_pair
 
@@ -367,7 +368,7 @@ def route_dispatch(routing_logits, routing_bias, local_expert_offset, routed_sca
     with torch.cuda.device(dev):
         code = _lib.load().moe_fp8_route_dispatch(int(shape), lg.data_ptr(), b.data_ptr(), T, int(local_expert_offset),
                                                   float(routed_scaling_factor), ids.data_ptr(), w.data_ptr(),
-                                                  header.data_ptr(), perm_tok.data_ptr(), perm_w.data_ptr(),
-                                                  pair.data_ptr(), _stream(dev))
+                                                  header.data_ptr(), header.numel(), perm_tok.data_ptr(),
+                                                  perm_w.data_ptr(), pair.data_ptr(), _stream(dev))
     _lib.check(code, "moe_fp8_route_dispatch")
     return ids, w, header[:_lib.MOE_FP8_HEADER_WORDS], perm_tok, perm_w, pair

@@ -20,7 +20,8 @@ MOE_ERR_HIP = -5
 MOE_ERR_ARG = -6
 MOE_ERR_NOALLOC_SIZE = -7
 MOE_FP8_NOALLOC_MAX_TOKENS = 64
-MOE_FP8_MAX_TOKENS = 1 << 17
+MOE_FP8_MAX_TOKENS = 1 << 20      # the forward entry points
+MOE_FP8_MAX_TAP_TOKENS = 1 << 17  # every other entry point
 MOE_FP8_CHUNK_TOKENS = 1 << 14
 MOE_FP8_HEADER_WORDS = 128
 
@@ -44,8 +45,9 @@ SIGNATURES = {
     "moe_fp8_quantize_activations": (ctypes.c_int, [_P, _I64, _P, _P, _P]),
     "moe_fp8_router_logits": (ctypes.c_int, [_P, _P, _I64, _P, _P]),
     "moe_fp8_router_quantize": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P]),
-    "moe_fp8_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "moe_fp8_route_dispatch": (ctypes.c_int, [ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P, _P, _P,
+    "moe_fp8_dispatch": (ctypes.c_int, [_P, _P, _I64, _I64, _P, ctypes.c_size_t, _P, _P, _P, _P]),
+    "moe_fp8_route_dispatch": (ctypes.c_int, [ctypes.c_int, _P, _P, _I64, _I64, ctypes.c_double, _P, _P, _P,
+                                              ctypes.c_size_t, _P, _P,
                                               _P, _P]),
     "moe_fp8_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "moe_fp8_last_hip_error": (ctypes.c_char_p, []),

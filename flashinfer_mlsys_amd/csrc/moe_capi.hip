@@ -12,8 +12,12 @@
 
 namespace moe {
 hipError_t launch_route(const float*, const uint16_t*, int, float, int32_t*, float*, int32_t*, hipStream_t);
+hipError_t launch_route_count(const float*, const uint16_t*, int, float, int, int32_t*, float*, int32_t*, int32_t*,
+                              hipStream_t);
 hipError_t launch_dispatch(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
                            int32_t*, hipStream_t);
+hipError_t launch_dispatch_scatter(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*,
+                                   int32_t*, const int32_t*, hipStream_t);
 hipError_t launch_dispatch_small(const int32_t*, const float*, int, int, DispatchHeader*, int32_t*, float*, int32_t*,
                                  hipStream_t);
 hipError_t launch_gemm1_decode(const float*, const uint16_t*, float, bool, const uint8_t*, const float*, int, int,
@@ -158,10 +162,12 @@ hipError_t run_stage(int stage, const Call& c) {
       if (c.decode && c.T <= kRouteInGemm1MaxTokens) return hipSuccess;  // routed inside GEMM1
       if (c.decode) return launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, nullptr, c.stream);
       {
-        hipError_t e = launch_route(c.logits, c.bias, c.T, c.rsf, c.topk_ids, c.topk_w, c.tok_pair, c.stream);
+        // routing + the count rows in one launch, then the scatter
+        hipError_t e = launch_route_count(c.logits, c.bias, c.T, c.rsf, c.offset, c.topk_ids, c.topk_w, c.tok_pair,
+                                          c.chunk_counts, c.stream);
         if (e != hipSuccess) return e;
-        return launch_dispatch(c.topk_ids, c.topk_w, c.T, c.offset, c.hdr, c.perm_tok, c.perm_w, c.tok_pair,
-                               c.chunk_counts, c.stream);
+        return launch_dispatch_scatter(c.topk_ids, c.topk_w, c.T, c.offset, c.hdr, c.perm_tok, c.perm_w, c.tok_pair,
+                                       c.chunk_counts, c.stream);
       }
     case 1:
       if (c.decode) {
@@ -261,7 +267,7 @@ int moe_fp8_run_stage(int stage, int shape, const float* routing_logits, const u
 int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                   double routed_scaling_factor, int32_t* topk_ids, float* topk_w, int32_t* tok_pair,
                   void* stream) {
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!routing_logits || !routing_bias || !topk_ids || !topk_w) return MOE_ERR_NULL;
   if (!aligned16(routing_logits) || !aligned16(routing_bias) || !aligned16(topk_ids) || !aligned16(topk_w) ||
@@ -273,8 +279,10 @@ int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int
 }
 
 int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, int64_t local_expert_offset,
-                     int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair, void* stream) {
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+                     int32_t* header, size_t header_words, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
+                     void* stream) {
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
+  if (header && header_words < (size_t)MOE_FP8_DISPATCH_HEADER_WORDS(T)) return MOE_ERR_WORKSPACE;
   if (!header || !perm_tok || !perm_w || !tok_pair || (T > 0 && (!topk_ids || !topk_w))) return MOE_ERR_NULL;
   if (!aligned16(header) || !aligned16(perm_tok) || !aligned16(perm_w) || !aligned16(tok_pair) ||
       (T > 0 && (!aligned16(topk_ids) || !aligned16(topk_w))))
@@ -287,11 +295,12 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
 
 int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                            int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
-                           float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
-                           void* stream) {
+                           float* topk_w, int32_t* header, size_t header_words, int32_t* perm_tok, float* perm_w,
+                           int32_t* tok_pair, void* stream) {
   using namespace moe;
   if (shape != MOE_SHAPE_AUTO && shape != MOE_SHAPE_PREFILL) return MOE_ERR_ARG;
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
+  if (header && header_words < (size_t)MOE_FP8_DISPATCH_HEADER_WORDS(T)) return MOE_ERR_WORKSPACE;
   if (T == 0) return MOE_OK;
   if (!routing_logits || !routing_bias || !topk_ids || !topk_w || !header || !perm_tok || !perm_w || !tok_pair)
     return MOE_ERR_NULL;
@@ -304,18 +313,22 @@ int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_
   auto* hdr = reinterpret_cast<DispatchHeader*>(header);
   hipError_t e;
   const bool decode = shape == MOE_SHAPE_AUTO && t <= kDecodeMaxTokens;
-  e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, decode ? nullptr : tok_pair, s);
-  if (e == hipSuccess) {
-    e = decode ? launch_dispatch_small(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s)
-               : launch_dispatch(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, header + MOE_FP8_HEADER_WORDS,
-                                 s);
+  if (decode) {
+    e = launch_route(routing_logits, routing_bias, t, rsf, topk_ids, topk_w, nullptr, s);
+    if (e == hipSuccess) e = launch_dispatch_small(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair, s);
+  } else {
+    e = launch_route_count(routing_logits, routing_bias, t, rsf, off, topk_ids, topk_w, tok_pair,
+                           header + MOE_FP8_HEADER_WORDS, s);
+    if (e == hipSuccess)
+      e = launch_dispatch_scatter(topk_ids, topk_w, t, off, hdr, perm_tok, perm_w, tok_pair,
+                                  header + MOE_FP8_HEADER_WORDS, s);
   }
   return e == hipSuccess ? MOE_OK : hip_fail(e);
 }
 
 int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t* hidden_states,
                                  float* hidden_states_scale, void* stream) {
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!hidden_bf16 || !hidden_states || !hidden_states_scale) return MOE_ERR_NULL;
   if (!aligned16(hidden_bf16) || !aligned16(hidden_states) || !aligned16(hidden_states_scale)) return MOE_ERR_ALIGN;
@@ -326,7 +339,7 @@ int moe_fp8_quantize_activations(const uint16_t* hidden_bf16, int64_t T, uint8_t
 
 int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
                           float* routing_logits, void* stream) {
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!hidden_bf16 || !gate_weight || !routing_logits) return MOE_ERR_NULL;
   if (!aligned16(hidden_bf16) || !aligned16(gate_weight) || !aligned16(routing_logits)) return MOE_ERR_ALIGN;
@@ -337,7 +350,7 @@ int moe_fp8_router_logits(const uint16_t* hidden_bf16, const uint16_t* gate_weig
 
 int moe_fp8_router_quantize(const uint16_t* hidden_bf16, const uint16_t* gate_weight, int64_t T,
                             float* routing_logits, uint8_t* hidden_states, float* hidden_states_scale, void* stream) {
-  if (T < 0 || T > MOE_FP8_MAX_TOKENS) return MOE_ERR_SIZE;
+  if (T < 0 || T > MOE_FP8_MAX_TAP_TOKENS) return MOE_ERR_SIZE;
   if (T == 0) return MOE_OK;
   if (!hidden_bf16 || !gate_weight || !routing_logits || !hidden_states || !hidden_states_scale) return MOE_ERR_NULL;
   if (!aligned16(hidden_bf16) || !aligned16(gate_weight) || !aligned16(routing_logits) || !aligned16(hidden_states) ||
@@ -420,6 +433,6 @@ const char* moe_fp8_strerror(int code) {
 
 const char* moe_fp8_last_hip_error(void) { return t_last_hip_error; }
 
-int moe_fp8_abi_version(void) { return 2; }
+int moe_fp8_abi_version(void) { return 3; }
 
 }  // extern "C"

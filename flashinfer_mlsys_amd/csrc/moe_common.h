@@ -106,13 +106,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 
 __host__ __device__ constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Dispatch (prefill shape) works on chunks of this many tokens and exchanges
-// 32 counts per chunk between its two kernels.
+// Dispatch (prefill shape): the routing kernel counts, per group of
+// COUNT_ROW_TOKENS tokens (one workgroup), the tokens that selected each local
+// expert (a row of 32 counts); the scatter kernel works on chunks of
+// DISPATCH_CHUNK tokens and sums the rows of all groups and of those before it.
 constexpr int DISPATCH_CHUNK = 256;
+constexpr int COUNT_ROW_TOKENS = 16;
 __host__ __device__ constexpr int dispatch_chunks(int64_t T) { return (int)((T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK); }
+__host__ __device__ constexpr int count_rows(int64_t T) { return (int)((T + COUNT_ROW_TOKENS - 1) / COUNT_ROW_TOKENS); }
 
 // Workspace layout for T tokens (worst case P = 8T routed pairs). The fp32
-// partial rows and the dispatch's chunk counts come last: only the prefill
+// partial rows and the dispatch's count rows come last: only the prefill
 // kernels use them, so a decode-shape call needs `total` bytes of make(T, false)
 // (the same offsets, without those regions).
 struct WorkspaceLayout {
@@ -130,7 +134,7 @@ struct WorkspaceLayout {
     L.perm_w = o;   o += align_up(P * 4, 256);
     L.c_act = o;    o += align_up(P * I * 2, 256);
     L.partial = o;  o += with_partial ? align_up(P * H * 4, 256) : 0;
-    L.chunk_counts = o; o += with_partial ? align_up((size_t)dispatch_chunks(T) * E_LOCAL * 4, 256) : 0;
+    L.chunk_counts = o; o += with_partial ? align_up((size_t)count_rows(T) * E_LOCAL * 4, 256) : 0;
     L.total = o;
     return L;
   }

@@ -786,7 +786,7 @@ static_assert(P1_BM * BLK == 4 * P1_WAVES * 1024 && P1_B_BYTES == 4 * P1_WAVES *
               "4 half fragments of each operand per wave");
 static_assert(P1_NT % P1_TBN == 0 && P1_TBM * P1_TBN == 32, "block order");
 static_assert(P1_LDS + (int)sizeof(TileMap) <= 160 * 1024, "LDS");
-static_assert((size_t)MOE_FP8_MAX_TOKENS * H < (1ull << 32) && (size_t)E_LOCAL * N1 * H < (1ull << 32) &&
+static_assert((size_t)MOE_FP8_CHUNK_TOKENS * H < (1ull << 32) && (size_t)E_LOCAL * N1 * H < (1ull << 32) &&
                   (size_t)E_LOCAL * NB_N1 * NB_H * 4 < (1ull << 32),
               "32-bit load offsets");
 

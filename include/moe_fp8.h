@@ -24,9 +24,11 @@ extern "C" {
 enum {
   MOE_OK = 0,
   MOE_ERR_NULL = -1,      /* a required pointer is NULL */
-  MOE_ERR_SIZE = -2,      /* T < 0 or T beyond MOE_FP8_MAX_TOKENS */
+  MOE_ERR_SIZE = -2,      /* T < 0 or T beyond MOE_FP8_MAX_TOKENS (MOE_FP8_MAX_TAP_TOKENS for the
+                             entry points other than the forward) */
   MOE_ERR_ALIGN = -3,     /* a pointer is not 16-byte aligned */
-  MOE_ERR_WORKSPACE = -4, /* workspace_bytes < moe_fp8_workspace_size(T) */
+  MOE_ERR_WORKSPACE = -4, /* workspace_bytes < moe_fp8_workspace_size(T), or a dispatch
+                             header shorter than MOE_FP8_DISPATCH_HEADER_WORDS(T) */
   MOE_ERR_HIP = -5,       /* a HIP launch failed; see moe_fp8_last_hip_error() */
   MOE_ERR_ARG = -6,       /* an enumerated argument (stage, shape) is out of range */
   MOE_ERR_NOALLOC_SIZE = -7 /* T beyond MOE_FP8_NOALLOC_MAX_TOKENS in moe_fp8_forward_noalloc */
@@ -37,8 +39,12 @@ enum {
  * T <= 64 and the prefill kernels above (AUTO), or the prefill kernels at any T. */
 enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
-/* Largest T any entry point accepts. */
-#define MOE_FP8_MAX_TOKENS (1 << 17)
+/* Largest T the forward entry points accept (they run calls above
+ * MOE_FP8_CHUNK_TOKENS chunk by chunk), and the largest T of every other entry
+ * point (routing, dispatch, the producer-side kernels), whose 32-bit offsets
+ * cover T * 7168 * 2 bytes. */
+#define MOE_FP8_MAX_TOKENS (1 << 20)
+#define MOE_FP8_MAX_TAP_TOKENS (1 << 17)
 
 /* Forward calls above this many tokens run the operator over consecutive token
  * chunks of this size (the last one shorter), in one chunk's workspace: the
@@ -49,9 +55,11 @@ enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
 /* Words of the `header` buffer moe_fp8_dispatch and moe_fp8_route_dispatch take
  * for T tokens: the dispatch header (MOE_FP8_HEADER_WORDS) followed by 32 counts
- * per chunk of 256 tokens, which the two dispatch kernels exchange. */
+ * per group of 16 tokens, which the counting and the scatter kernels exchange.
+ * Both entry points take the buffer's size and return MOE_ERR_WORKSPACE when it
+ * is shorter than this. */
 #define MOE_FP8_HEADER_WORDS 128
-#define MOE_FP8_DISPATCH_HEADER_WORDS(T) (MOE_FP8_HEADER_WORDS + 32 * (((T) + 255) / 256))
+#define MOE_FP8_DISPATCH_HEADER_WORDS(T) (MOE_FP8_HEADER_WORDS + 32 * (((T) + 15) / 16))
 
 /* Bytes of device workspace one forward call needs for T tokens (worst case
  * of 8 routed local pairs per token; for T above MOE_FP8_CHUNK_TOKENS the size
@@ -164,7 +172,8 @@ int moe_fp8_route(const float* routing_logits, const uint16_t* routing_bias, int
  *            entry (moe_fp8_route sets that), local slots are overwritten.
  */
 int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, int64_t local_expert_offset,
-                     int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair, void* stream);
+                     int32_t* header, size_t header_words, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
+                     void* stream);
 
 /*
  * Routing and dispatch as moe_fp8_forward_shape(shape, ...) runs them (in the
@@ -176,8 +185,8 @@ int moe_fp8_dispatch(const int32_t* topk_ids, const float* topk_w, int64_t T, in
  */
 int moe_fp8_route_dispatch(int shape, const float* routing_logits, const uint16_t* routing_bias, int64_t T,
                            int64_t local_expert_offset, double routed_scaling_factor, int32_t* topk_ids,
-                           float* topk_w, int32_t* header, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
-                           void* stream);
+                           float* topk_w, int32_t* header, size_t header_words, int32_t* perm_tok, float* perm_w,
+                           int32_t* tok_pair, void* stream);
 
 /*
  * Producer-side FP8 activation quantiser (the step before this operator:

@@ -37,7 +37,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strings(lib):
-    assert lib.moe_fp8_abi_version() == 2
+    assert lib.moe_fp8_abi_version() == 3
     for code in (0, -1, -2, -3, -4, -5, -6, -7):
         assert lib.moe_fp8_strerror(code)
     assert lib.moe_fp8_strerror(-99) == b"unknown error"
@@ -74,6 +74,8 @@ def _fwd(lib, T=1, ptrs=None, ws_bytes=1 << 40):
 def test_forward_argument_errors(lib):
     assert _fwd(lib, T=-1) == _lib.MOE_ERR_SIZE
     assert _fwd(lib, T=_lib.MOE_FP8_MAX_TOKENS + 1) == _lib.MOE_ERR_SIZE
+    # the forward runs long calls chunk by chunk: beyond the other entry points' limit is fine
+    assert _fwd(lib, T=_lib.MOE_FP8_MAX_TAP_TOKENS + 1, ws_bytes=1) == _lib.MOE_ERR_WORKSPACE
     assert _fwd(lib, T=0) == _lib.MOE_OK
     ptrs = [FAKE] * 8
     ptrs[3] = None
@@ -104,15 +106,30 @@ def test_route_and_dispatch_argument_errors(lib):
     assert lib.moe_fp8_route(None, FAKE, 4, 2.5, FAKE, FAKE, None, None) == _lib.MOE_ERR_NULL
     assert lib.moe_fp8_route(FAKE + 8, FAKE, 4, 2.5, FAKE, FAKE, None, None) == _lib.MOE_ERR_ALIGN
     assert lib.moe_fp8_route(FAKE, FAKE, -3, 2.5, FAKE, FAKE, None, None) == _lib.MOE_ERR_SIZE
-    assert lib.moe_fp8_dispatch(FAKE, FAKE, 4, 0, None, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_NULL
-    assert lib.moe_fp8_dispatch(FAKE, FAKE, 4, 0, FAKE + 4, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_ALIGN
+    hw = _lib.MOE_FP8_HEADER_WORDS + 32
+    assert lib.moe_fp8_dispatch(FAKE, FAKE, 4, 0, None, hw, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_NULL
+    assert lib.moe_fp8_dispatch(FAKE, FAKE, 4, 0, FAKE + 4, hw, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_ALIGN
+    assert lib.moe_fp8_route(FAKE, FAKE, _lib.MOE_FP8_MAX_TAP_TOKENS + 1, 2.5, FAKE, FAKE, None, None) == \
+        _lib.MOE_ERR_SIZE
+
+
+def test_dispatch_header_size_checked(lib):
+    """The dispatch taps take the header's size: the header words, then 32 counts per
+    group of 16 tokens; one word short is rejected before any GPU call."""
+    for T in (1, 16, 17, 300, 4097):
+        need = _lib.MOE_FP8_HEADER_WORDS + 32 * ((T + 15) // 16)
+        assert lib.moe_fp8_dispatch(FAKE, FAKE, T, 0, FAKE, need - 1, FAKE, FAKE, FAKE, None) == \
+            _lib.MOE_ERR_WORKSPACE
+        for shape in (_lib.MOE_SHAPE_AUTO, _lib.MOE_SHAPE_PREFILL):
+            assert lib.moe_fp8_route_dispatch(shape, FAKE, FAKE, T, 0, 2.5, FAKE, FAKE, FAKE, need - 1, FAKE, FAKE,
+                                              FAKE, None) == _lib.MOE_ERR_WORKSPACE
 
 
 def test_quantize_argument_errors(lib):
     q = lib.moe_fp8_quantize_activations
     assert q(FAKE, 0, FAKE, FAKE, None) == _lib.MOE_OK
     assert q(FAKE, -1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert q(FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert q(FAKE, _lib.MOE_FP8_MAX_TAP_TOKENS + 1, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
     assert q(None, 4, FAKE, FAKE, None) == _lib.MOE_ERR_NULL
     assert q(FAKE, 4, FAKE, None, None) == _lib.MOE_ERR_NULL
     assert q(FAKE, 4, FAKE + 8, FAKE, None) == _lib.MOE_ERR_ALIGN
@@ -122,7 +139,7 @@ def test_router_argument_errors(lib):
     r = lib.moe_fp8_router_logits
     assert r(FAKE, FAKE, 0, None, None) == _lib.MOE_OK  # nothing to do, nothing read
     assert r(FAKE, FAKE, -1, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TAP_TOKENS + 1, FAKE, None) == _lib.MOE_ERR_SIZE
     assert r(None, FAKE, 4, FAKE, None) == _lib.MOE_ERR_NULL
     assert r(FAKE, None, 4, FAKE, None) == _lib.MOE_ERR_NULL
     assert r(FAKE, FAKE, 4, None, None) == _lib.MOE_ERR_NULL
@@ -134,7 +151,7 @@ def test_router_quantize_argument_errors(lib):
     r = lib.moe_fp8_router_quantize
     assert r(FAKE, FAKE, 0, None, None, None, None) == _lib.MOE_OK  # nothing to do, nothing read
     assert r(FAKE, FAKE, -1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
-    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TOKENS + 1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
+    assert r(FAKE, FAKE, _lib.MOE_FP8_MAX_TAP_TOKENS + 1, FAKE, FAKE, FAKE, None) == _lib.MOE_ERR_SIZE
     for i in range(5):
         args = [FAKE] * 5
         args[i] = None
@@ -151,7 +168,8 @@ def test_shape_argument(lib):
     for bad in (-1, 2, 7):
         assert lib.moe_fp8_forward_shape(bad, *args) == _lib.MOE_ERR_ARG
         assert lib.moe_fp8_run_stage(0, bad, *args) == _lib.MOE_ERR_ARG
-        assert lib.moe_fp8_route_dispatch(bad, FAKE, FAKE, 4, 0, 2.5, *[FAKE] * 6, None) == _lib.MOE_ERR_ARG
+        assert lib.moe_fp8_route_dispatch(bad, FAKE, FAKE, 4, 0, 2.5, FAKE, FAKE, FAKE, 1 << 20, *[FAKE] * 3,
+                                          None) == _lib.MOE_ERR_ARG
     for stage in (-1, 4):
         assert lib.moe_fp8_run_stage(stage, 0, *args) == _lib.MOE_ERR_ARG
     for shape in (_lib.MOE_SHAPE_AUTO, _lib.MOE_SHAPE_PREFILL):  # valid shape: the usual checks follow
