@@ -85,7 +85,7 @@ class Case:
         self.E_act = int((counts > 0).sum())
         self.flops, self.bytes = wl.algorithmic_counts(self.P, self.E_act, self.T)
         self.gemm1_bytes = self.E_act * W13_BYTES + self.P * (wl.H + wl.NB_H * 4 + wl.I * 2)
-        # decode GEMM2 sums each token's pairs itself: bf16 rows out, no fp32 partial rows
+        # decode GEMM2 sums each token's pairs itself: bf16 rows out, no pair rows
         self.gemm2_bytes = self.E_act * W2_BYTES + self.P * wl.I * 2 + self.T * wl.H * 2
 
 

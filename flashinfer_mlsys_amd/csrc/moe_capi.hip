@@ -32,8 +32,8 @@ int gemm1_decode_blocks_per_cu();
 hipError_t launch_gemm1_prefill(const uint8_t*, const float*, int, const uint8_t*, const float*,
                                const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
-                               float*, int, hipStream_t);
-hipError_t launch_combine(const float*, const int32_t*, int, uint16_t*, hipStream_t);
+                               uint16_t*, int, hipStream_t);
+hipError_t launch_combine(const uint16_t*, const int32_t*, int, uint16_t*, hipStream_t);
 }  // namespace moe
 
 namespace {
@@ -95,8 +95,8 @@ struct Call {
   hipStream_t stream;
   moe::DispatchHeader* hdr;
   int32_t *topk_ids, *tok_pair, *perm_tok, *chunk_counts;
-  float *topk_w, *perm_w, *partial;
-  uint16_t* c_act;
+  float *topk_w, *perm_w;
+  uint16_t *c_act, *partial;  // fp16: C * 2^-8 and the pair rows w * O * 2^-8
 };
 
 int check_call(const float* routing_logits, const uint16_t* routing_bias, const uint8_t* hidden_states,
@@ -143,7 +143,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
   c.perm_tok = reinterpret_cast<int32_t*>(ws + L.perm_tok);
   c.perm_w = reinterpret_cast<float*>(ws + L.perm_w);
   c.c_act = reinterpret_cast<uint16_t*>(ws + L.c_act);
-  c.partial = reinterpret_cast<float*>(ws + L.partial);
+  c.partial = reinterpret_cast<uint16_t*>(ws + L.partial);
   c.chunk_counts = reinterpret_cast<int32_t*>(ws + L.chunk_counts);
   return 1;  // valid, work to do
 }
@@ -151,7 +151,7 @@ int check_call(const float* routing_logits, const uint16_t* routing_bias, const 
 // Stage 0: routing (+ dispatch in the prefill shape; nothing for a decode call
 // of at most 8 tokens, routed inside GEMM1); 1: GEMM1 + SwiGLU (+ the
 // in-workgroup dispatch in the decode shape); 2: GEMM2 x weight (prefill: into
-// one fp32 row per pair; decode: with the ordered per-token sum, straight to the
+// one fp16 row per pair; decode: with the ordered per-token sum, straight to the
 // bf16 output); 3: the ordered combine of the prefill rows to bf16 (nothing in
 // the decode shape).
 hipError_t run_stage(int stage, const Call& c) {

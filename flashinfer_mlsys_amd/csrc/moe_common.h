@@ -115,10 +115,10 @@ constexpr int COUNT_ROW_TOKENS = 16;
 __host__ __device__ constexpr int dispatch_chunks(int64_t T) { return (int)((T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK); }
 __host__ __device__ constexpr int count_rows(int64_t T) { return (int)((T + COUNT_ROW_TOKENS - 1) / COUNT_ROW_TOKENS); }
 
-// Workspace layout for T tokens (worst case P = 8T routed pairs). The fp32
-// partial rows and the dispatch's count rows come last: only the prefill
-// kernels use them, so a decode-shape call needs `total` bytes of make(T, false)
-// (the same offsets, without those regions).
+// Workspace layout for T tokens (worst case P = 8T routed pairs). The pair rows
+// (fp16 of w * O * 2^-8, one per pair) and the dispatch's count rows come last:
+// only the prefill kernels use them, so a decode-shape call needs `total` bytes
+// of make(T, false) (the same offsets, without those regions).
 struct WorkspaceLayout {
   size_t hdr = 0, topk_ids = 0, topk_w = 0, tok_pair = 0, perm_tok = 0, perm_w = 0, c_act = 0, partial = 0,
          chunk_counts = 0, total = 0;
@@ -133,7 +133,7 @@ struct WorkspaceLayout {
     L.perm_tok = o; o += align_up(P * 4, 256);
     L.perm_w = o;   o += align_up(P * 4, 256);
     L.c_act = o;    o += align_up(P * I * 2, 256);
-    L.partial = o;  o += with_partial ? align_up(P * H * 4, 256) : 0;
+    L.partial = o;  o += with_partial ? align_up(P * H * 2, 256) : 0;
     L.chunk_counts = o; o += with_partial ? align_up((size_t)count_rows(T) * E_LOCAL * 4, 256) : 0;
     L.total = o;
     return L;

@@ -6,7 +6,7 @@
 //   GEMM2  O  = C . W2_e^T           [cnt, 2048] x [2048, 7168]  (ref_moe.py:161-162)
 //   weight O * w[token, e]; out[t] = sum over t's local experts in ascending id,
 //   then bf16 (ref_moe.py:164-168): in the decode shape inside GEMM2, in the
-//   prefill shape through one fp32 row per (token, expert) pair and the combine
+//   prefill shape through one row per (token, expert) pair and the combine
 //
 // GEMM1 runs on the e4m3 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0
 // scales). One MFMA covers exactly one 128-wide K block, so the fp32 block
@@ -1185,7 +1185,7 @@ struct G2Item {
 template <int NI>
 __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot, int wm, int wn, int lane,
                                                const G2Item& it, const float* __restrict__ perm_w,
-                                               float* __restrict__ partial) {
+                                               uint16_t* __restrict__ partial) {
   const int lr = lane & 31, lg = lane >> 5;
   v16f acc[2][2];
 #pragma unroll
@@ -1243,7 +1243,9 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this block's LDS reads are done
   }
-  // epilogue: weight by the pair's routing weight, one fp32 row per pair. The
+  // epilogue: weight by the pair's routing weight, one row per pair, stored as
+  // fp16 of w * O * 2^-8 (c_encode: 11 significant bits, the encoding of C; the
+  // combine sums the decoded rows in fp32). The
   // weights of a row block's 32 rows are uniform over the wave and read with
   // scalar loads (counted by lgkmcnt), so no wait covers the stores before them:
   // a vector load here would wait, on vmcnt, for every store in flight. Rows past
@@ -1263,9 +1265,9 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
       const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
       if (row < it.cnt) {
         const float w = lg ? wh[r] : wl[r];
-        float* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
+        uint16_t* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[j * 32] = acc[i][j][r] * w;
+        for (int j = 0; j < 2; ++j) dst[j * 32] = c_encode(acc[i][j][r] * w);
       }
     }
   }
@@ -1273,7 +1275,7 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
 
 __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, float* __restrict__ partial) {
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, uint16_t* __restrict__ partial) {
   extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
   __shared__ TileMap map;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1420,35 +1422,79 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Ordered combine: out[t] = bf16( sum_j partial[pair(t, j)] ) over t's local
-// experts in ascending id; zeros for tokens with none. The fp32 pair rows are
-// read once: non-temporal loads, which leave the caches (the 256 MB memory-side
-// cache above all) to data that is used again, such as the expert weights.
+// Ordered combine: out[t] = bf16( sum_j pair row(t, j) ) over t's local experts
+// in ascending id, the rows decoded from fp16 (x 2^8, exact) and summed in fp32;
+// zeros for tokens with none. Each lane takes 8 columns, one 16 B load per pair.
+// The token's pair slots that hold a local pair (a uniform bit set) fix the
+// number N of loads; a body compiled for each N issues its N loads together and
+// then sums (with a branch per slot the compiler waited for each load before
+// issuing the next; with all 8 slots loading, a mostly empty token paid for 8
+// load instructions). The pair rows are read once: non-temporal loads, which
+// leave the caches (the 256 MB memory-side cache above all) to data that is
+// used again, such as the expert weights.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
-                                                      const int32_t* __restrict__ tok_pair, int T,
-                                                      uint16_t* __restrict__ out) {
-  // workgroup (t, c): token t, columns 1024 c .. 1024 c + 1023, 4 per thread
-  const int t = blockIdx.x, h = blockIdx.y * 1024 + threadIdx.x * 4;
-  int p[TOP_K];
+constexpr int CPOL_NT = 2;  // cache-policy operand of the buffer-load builtins: non-temporal
+constexpr int COMBINE_THREADS = 128;
+constexpr int COMBINE_COLS = 8 * COMBINE_THREADS;  // 1024 columns per workgroup
+static_assert(H % COMBINE_COLS == 0, "the combine grid covers H");
+
+// The N pairs of slot set m (ascending slots), summed into acc.
+template <int N>
+__device__ __forceinline__ void combine_pairs(const uint16_t* __restrict__ partial, const int (&p)[TOP_K], uint32_t m,
+                                              float (&acc)[8]) {
+  v4i v[N];  // 8 fp16 values each
 #pragma unroll
-  for (int j = 0; j < TOP_K; ++j) p[j] = tok_pair[(size_t)t * TOP_K + j];
-  v4f v[TOP_K];
+  for (int k = 0; k < N; ++k) {
+    const int slot = __builtin_ctz(m);  // uniform
+    m &= m - 1u;
+    int pr = p[0];
+#pragma unroll
+    for (int j = 1; j < TOP_K; ++j) pr = slot == j ? p[j] : pr;
+    const __amdgpu_buffer_rsrc_t r = buf_rsrc(partial + (size_t)pr * H + blockIdx.y * COMBINE_COLS,
+                                              COMBINE_COLS * (uint32_t)sizeof(uint16_t));
+    v[k] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, threadIdx.x * 16u, 0, CPOL_NT));
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // (halves taken with shifts: __builtin_bit_cast of a vector element such
+      // as v[k][q] reads element 0 on this compiler)
+      const uint32_t w = (uint32_t)v[k][q];
+      acc[2 * q] += (float)__builtin_bit_cast(_Float16, (uint16_t)w) * C_LOAD_SCALE;
+      acc[2 * q + 1] += (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)) * C_LOAD_SCALE;
+    }
+}
+
+__global__ __launch_bounds__(COMBINE_THREADS) void combine_kernel(const uint16_t* __restrict__ partial,
+                                                                  const int32_t* __restrict__ tok_pair, int T,
+                                                                  uint16_t* __restrict__ out) {
+  // workgroup (t, c): token t, columns 1024 c .. 1024 c + 1023, 8 per thread
+  const int t = blockIdx.x, h = blockIdx.y * COMBINE_COLS + threadIdx.x * 8;
+  int p[TOP_K];
+  uint32_t m = 0;  // slots holding a local pair
 #pragma unroll
   for (int j = 0; j < TOP_K; ++j) {
-    v[j] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (p[j] >= 0) v[j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(partial + (size_t)p[j] * H + h));
+    p[j] = tok_pair[(size_t)t * TOP_K + j];
+    m |= (p[j] >= 0 ? 1u : 0u) << j;
   }
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  switch (__popc(m)) {  // uniform
+    case 0: break;
+    case 1: combine_pairs<1>(partial, p, m, acc); break;
+    case 2: combine_pairs<2>(partial, p, m, acc); break;
+    case 3: combine_pairs<3>(partial, p, m, acc); break;
+    case 4: combine_pairs<4>(partial, p, m, acc); break;
+    case 5: combine_pairs<5>(partial, p, m, acc); break;
+    case 6: combine_pairs<6>(partial, p, m, acc); break;
+    case 7: combine_pairs<7>(partial, p, m, acc); break;
+    default: combine_pairs<8>(partial, p, m, acc); break;
+  }
+  v4i o;
 #pragma unroll
-  for (int j = 0; j < TOP_K; ++j)  // ascending slot = ascending expert id
-    if (p[j] >= 0) {
-      acc.x += v[j][0]; acc.y += v[j][1]; acc.z += v[j][2]; acc.w += v[j][3];
-    }
-  uint2 o;
-  o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-  o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-  *reinterpret_cast<uint2*>(out + (size_t)t * H + h) = o;
+  for (int q = 0; q < 4; ++q)
+    o[q] = (int)((uint32_t)f32_to_bf16_rne(acc[2 * q]) | ((uint32_t)f32_to_bf16_rne(acc[2 * q + 1]) << 16));
+  *reinterpret_cast<v4i*>(out + (size_t)t * H + h) = o;
 }
 
 }  // namespace moe
@@ -1520,7 +1566,7 @@ hipError_t launch_gemm1_prefill(const uint8_t* hidden, const float* hscale, int 
 }
 
 hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
-                               const float* perm_w, float* partial, int grid, hipStream_t stream) {
+                               const float* perm_w, uint16_t* partial, int grid, hipStream_t stream) {
   static PerDeviceOnce<hipError_t> once;
   hipError_t e = hipErrorInvalidDevice;
   once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm2_loader_kernel),
@@ -1532,10 +1578,10 @@ hipError_t launch_gemm2_loader(const uint16_t* c_act, const uint8_t* w2, const f
   return hipGetLastError();
 }
 
-hipError_t launch_combine(const float* partial, const int32_t* tok_pair, int T, uint16_t* out, hipStream_t stream) {
+hipError_t launch_combine(const uint16_t* partial, const int32_t* tok_pair, int T, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  static_assert(H % 1024 == 0, "combine chunks");
-  hipLaunchKernelGGL(combine_kernel, dim3(T, H / 1024), dim3(256), 0, stream, partial, tok_pair, T, out);
+  hipLaunchKernelGGL(combine_kernel, dim3(T, H / COMBINE_COLS), dim3(COMBINE_THREADS), 0, stream, partial, tok_pair, T,
+                     out);
   return hipGetLastError();
 }
 

@@ -48,9 +48,10 @@ enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
 
 /* Forward calls above this many tokens run the operator over consecutive token
  * chunks of this size (the last one shorter), in one chunk's workspace: the
- * worst-case workspace (8 local pairs per token, fp32 rows of every pair) is
- * about 262 KB per token, 4.3 GB for one chunk. Tokens are independent, so the
- * output is bit for bit the unchunked one. */
+ * worst-case workspace (8 local pairs per token, an fp16 row of C and of the
+ * weighted GEMM2 output for every pair) is about 144 KB per token, 2.4 GB for
+ * one chunk. Tokens are independent, so the output is bit for bit the
+ * unchunked one. */
 #define MOE_FP8_CHUNK_TOKENS (1 << 14)
 
 /* Words of the `header` buffer moe_fp8_dispatch and moe_fp8_route_dispatch take

@@ -57,8 +57,8 @@ def test_workspace_size(lib):
     for T in (1, 2, 16, 1024, 8192):
         n = lib.moe_fp8_workspace_size(T)
         assert n > prev
-        # at least the per-pair bf16 intermediate and fp32 partial rows
-        assert n >= 8 * T * (2048 * 2 + 7168 * 4)
+        # at least the per-pair fp16 C rows and fp16 pair rows
+        assert n >= 8 * T * (2048 * 2 + 7168 * 2)
         assert n % 256 == 0
         prev = n
 
@@ -87,7 +87,7 @@ def test_forward_argument_errors(lib):
     assert _fwd(lib, T=100, ws_bytes=lib.moe_fp8_workspace_size(100) - 1) == _lib.MOE_ERR_WORKSPACE
     assert lib.moe_fp8_forward_shape(_lib.MOE_SHAPE_PREFILL, *[FAKE] * 8, 16, 0, 2.5, FAKE, FAKE,
                                      lib.moe_fp8_workspace_size(16) - 1, None) == _lib.MOE_ERR_WORKSPACE
-    # the decode kernels (T <= 64) use no fp32 partial rows: less is enough, but not a few bytes
+    # the decode kernels (T <= 64) use no pair rows: less is enough, but not a few bytes
     assert _fwd(lib, T=16, ws_bytes=4096) == _lib.MOE_ERR_WORKSPACE
 
 

@@ -434,15 +434,17 @@ def test_expert_row_counts_at_tile_edges_match_oracle(weights, dev, offset):
     assert_close_bf16(out, ref, f"edge counts offset={offset}")
 
 
-DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48]]
+DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48], [2, 3, 4, 5, 6, 7, 8, 9]]
 
 
-@pytest.mark.parametrize("counts", DECODE_EDGE_COUNTS, ids=["64", "33-31", "17-16-15-1-0-15", "1x32", "last48"])
+@pytest.mark.parametrize("counts", DECODE_EDGE_COUNTS,
+                         ids=["64", "33-31", "17-16-15-1-0-15", "1x32", "last48", "2-to-9"])
 @pytest.mark.parametrize("path", [fm.SHAPE_AUTO, fm.SHAPE_PREFILL], ids=["auto", "prefill"])
 def test_decode_row_counts_at_pass_edges_match_oracle(weights, dev, counts, path):
     """At most 64 tokens with the local rows packed on few experts (a 64-row
     expert, 16 / 17 / 31 / 33 rows, every expert with one row, only the last
-    expert): the decode kernels' 16-row passes and the prefill kernels (forced)
+    expert, 2 to 9 rows: the decode GEMM2's activation loads in one, two or three
+    steps): the decode kernels' 16-row passes and the prefill kernels (forced)
     both match the CPU oracle."""
     offset = 32
     lg, b = _routing_for_counts(counts, offset, 5151 + len(counts))
