@@ -532,57 +532,57 @@ def main():
     log(f"fm.kernel T=1: {wall_us:.1f} us wall per call, {gpu_us:.1f} us between events "
         f"(C ABI: {per_T[0]['us_per_call']} us)")
 
-    # the producer-side activation quantiser (bf16 -> e4m3 + [56, T] scales), HBM-bound
+    # The producer side: the activation quantiser (bf16 -> e4m3 + [56, T] scales,
+    # HBM-bound), the router GEMM (routing_logits = hidden_bf16 @ gate.T), both in
+    # one call, and the two as separate calls back to back. The four graphs are
+    # replayed in turn over several rounds and each figure is the median: a
+    # single replay right after building a graph reads 5-10 % slow (the clock
+    # settles over the first replays), enough to misorder the fused call and the
+    # separate ones.
     if not args.no_extra:
-        qa = {}
-        for T in (64, 8192):
-            x = wl.hidden_bf16(T, 77).to(dev)
-            qbuf = (torch.empty((T, wl.H), dtype=torch.float8_e4m3fn, device=dev),
-                    torch.empty((wl.NB_H, T), dtype=torch.float32, device=dev))
-            g = runner.graph(lambda: fm.quantize_activations(x, out=qbuf), args.reps)
-            us = runner.graph_us(g, args.reps)
-            del g
-            nbytes = T * (wl.H * 2 + wl.H + wl.NB_H * 4)
-            qa[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
-                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
-                            "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
-            log(f"quantize_activations T={T}: {us:.1f} us, {qa[f'T={T}']['GB_per_s']} GB/s")
-        also["quantize_activations"] = qa
-        # producer side: the router GEMM (routing_logits = hidden_bf16 @ gate.T)
-        rl = {}
+        qa, rl, rq = {}, {}, {}
         gate = wl.gate_weight_bf16().to(dev)
         for T in (64, 8192):
-            x = wl.hidden_bf16(T, 78).to(dev)
+            x = wl.hidden_bf16(T, 77).to(dev)
             lbuf = torch.empty((T, wl.E_GLOBAL), dtype=torch.float32, device=dev)
-            g = runner.graph(lambda: fm.router_logits(x, gate, out=lbuf), args.reps)
-            us = runner.graph_us(g, args.reps)
-            del g
-            nbytes = T * wl.H * 2 + wl.E_GLOBAL * wl.H * 2 + T * wl.E_GLOBAL * 4
-            flops = 2 * T * wl.E_GLOBAL * wl.H
-            rl[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
-                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
-                            "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
-                            "TFLOP_per_s": round(flops / (us * 1e-6) / 1e12, 1),
-                            "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
-            log(f"router_logits T={T}: {us:.1f} us, {rl[f'T={T}']['GB_per_s']} GB/s, "
-                f"{rl[f'T={T}']['TFLOP_per_s']} TFLOP/s")
-        also["router_logits"] = rl
-        # both producer steps in one pass over the hidden states
-        rq = {}
-        for T in (64, 8192):
-            x = wl.hidden_bf16(T, 79).to(dev)
-            bufs = (torch.empty((T, wl.E_GLOBAL), dtype=torch.float32, device=dev),
-                    torch.empty((T, wl.H), dtype=torch.float8_e4m3fn, device=dev),
+            qbuf = (torch.empty((T, wl.H), dtype=torch.float8_e4m3fn, device=dev),
                     torch.empty((wl.NB_H, T), dtype=torch.float32, device=dev))
-            g = runner.graph(lambda: fm.router_logits_and_quantize(x, gate, out=bufs), args.reps)
-            us = runner.graph_us(g, args.reps)
-            del g
-            nbytes = (T * wl.H * 2 + wl.E_GLOBAL * wl.H * 2 + T * wl.E_GLOBAL * 4
-                      + T * (wl.H + wl.NB_H * 4))
-            rq[f"T={T}"] = {"us_per_call": round(us, 2), "bytes": nbytes,
-                            "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1),
-                            "separate_us": round(rl[f"T={T}"]["us_per_call"] + qa[f"T={T}"]["us_per_call"], 2)}
-            log(f"router_logits_and_quantize T={T}: {us:.1f} us (separate kernels {rq[f'T={T}']['separate_us']} us)")
+            graphs = {
+                "quantize": runner.graph(lambda: fm.quantize_activations(x, out=qbuf), args.reps),
+                "router": runner.graph(lambda: fm.router_logits(x, gate, out=lbuf), args.reps),
+                "fused": runner.graph(lambda: fm.router_logits_and_quantize(x, gate, out=(lbuf, *qbuf)), args.reps),
+                "separate": runner.graph(lambda: (fm.router_logits(x, gate, out=lbuf),
+                                                  fm.quantize_activations(x, out=qbuf)), args.reps),
+            }
+            trials = {k: [] for k in graphs}
+            for _ in range(5):
+                for k, g in graphs.items():
+                    trials[k].append(runner.graph_us(g, args.reps))
+            del graphs
+            us = {k: statistics.median(v) for k, v in trials.items()}
+            qbytes = T * (wl.H * 2 + wl.H + wl.NB_H * 4)
+            qa[f"T={T}"] = {"us_per_call": round(us["quantize"], 2), "bytes": qbytes,
+                            "GB_per_s": round(qbytes / (us["quantize"] * 1e-6) / 1e9, 1),
+                            "hbm_frac": round(qbytes / (us["quantize"] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+            rbytes = T * wl.H * 2 + wl.E_GLOBAL * wl.H * 2 + T * wl.E_GLOBAL * 4
+            flops = 2 * T * wl.E_GLOBAL * wl.H
+            rl[f"T={T}"] = {"us_per_call": round(us["router"], 2), "bytes": rbytes,
+                            "GB_per_s": round(rbytes / (us["router"] * 1e-6) / 1e9, 1),
+                            "hbm_frac": round(rbytes / (us["router"] * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+                            "TFLOP_per_s": round(flops / (us["router"] * 1e-6) / 1e12, 1),
+                            "bf16_mfma_frac": round(flops / (us["router"] * 1e-6) / 2.5e15, 4)}
+            fbytes = rbytes + T * (wl.H + wl.NB_H * 4)
+            rq[f"T={T}"] = {"us_per_call": round(us["fused"], 2), "bytes": fbytes,
+                            "GB_per_s": round(fbytes / (us["fused"] * 1e-6) / 1e9, 1),
+                            "separate_calls_us": round(us["separate"], 2),
+                            "separate_alone_sum_us": round(us["router"] + us["quantize"], 2)}
+            log(f"quantize_activations T={T}: {us['quantize']:.1f} us, {qa[f'T={T}']['GB_per_s']} GB/s")
+            log(f"router_logits T={T}: {us['router']:.1f} us, {rl[f'T={T}']['GB_per_s']} GB/s, "
+                f"{rl[f'T={T}']['TFLOP_per_s']} TFLOP/s")
+            log(f"router_logits_and_quantize T={T}: {us['fused']:.1f} us (the two calls back to back "
+                f"{us['separate']:.1f} us; each timed alone, summed {us['router'] + us['quantize']:.1f} us)")
+        also["quantize_activations"] = qa
+        also["router_logits"] = rl
         also["router_logits_and_quantize"] = rq
 
     cpu = None
