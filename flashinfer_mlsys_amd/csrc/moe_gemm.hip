@@ -33,6 +33,7 @@
 //                consecutive items, which share operand tiles, so that XCD's L2
 //                serves the repeats.
 #include "moe_common.h"
+#include <type_traits>
 #include "moe_host.h"
 #include "moe_route_token.h"
 #include "moe_small_dispatch.h"
@@ -141,51 +142,28 @@ __device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __res
   for (int kk = 0; kk < D1_KPW; ++kk) b[kk] = load_v8i(wp + kk * BLK);
 }
 
-// This wave's K slice of rows m0..m0+15 of expert le (rows past cnt repeat the
-// last one) and their activation scales, staged into LDS (only this wave reads
-// them) in two steps so that a caller can issue other loads in between: the
-// loads into registers, then the LDS writes, which wait only for these loads.
-// Lane l's fragment bytes are row l % 16, K 32 (l / 16) + [0, 32): half h holds
-// bytes [16 h, 16 h + 16). Plain loads and ds_writes, no direct-to-LDS loads:
-// the compiler cannot tell which LDS bytes a direct load writes, so every later
-// LDS read would wait for all loads in flight, the weight prefetches included.
+// The first expert's activation rows for the prologue: this wave's K slice (7
+// K blocks = 896 B per row) of its first min(cnt, 16) rows and their scales,
+// staged into LDS (only this wave reads them) in two steps so that the weight
+// requests go out in between: the loads into registers, then the LDS writes,
+// which wait only for these loads. The rows travel compactly: load i, lane l
+// takes bytes 16 (64 i + l) of the rows' slices laid end to end (row r = byte /
+// 896, offset o = byte % 896 = 128 kk + 32 kg + 16 h), so NA loads cover
+// floor(1024 NA / 896) rows: 1 load for one row, 4 for four, 14 for sixteen,
+// instead of 14 loads of 16 rows that repeat the last one (the load path's time
+// per instruction is what these loads cost before the first weight request).
+// In LDS, lane (fr, kg)'s fragment bytes are row fr, K 32 kg + [0, 32): half h
+// holds bytes [16 h, 16 h + 16). Rows at or past cnt hold zeros or whatever the
+// LDS held; they reach only their own MFMA output rows, which are never stored.
+// Plain loads and ds_writes, no direct-to-LDS loads: the compiler cannot tell
+// which LDS bytes a direct load writes, so every later LDS read would wait for
+// all loads in flight, the weight prefetches included.
+constexpr int D1_ROW = D1_KPW * BLK;  // 896 B: a row's K slice for one wave
+template <int NA>
 struct G1AStage {
-  v4i rows[D1_KPW][2];
+  v4i rows[NA];
   float sc[2];
 };
-
-// (tok: the expert's ascending token list, at least min(cnt, m0 + 16) entries)
-__device__ __forceinline__ void g1_stage_a_load(G1AStage& a, const int* tok, int cnt,
-                                                const uint8_t* __restrict__ hidden,
-                                                const float* __restrict__ hscale, int T, int m0, int wave) {
-  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
-  const int kb0 = wave * D1_KPW;
-  // scales: entry i = 16 kk + r of the wave's block (lanes past 112 of the second load idle)
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int i = lane + 64 * j;
-    a.sc[j] = 0.f;
-    if (i < D1_KPW * 16) {
-      const int kk = i >> 4, r = i & 15;
-      a.sc[j] = hscale[(size_t)(kb0 + kk) * T + tok[min(m0 + r, cnt - 1)]];
-    }
-  }
-  const uint8_t* ap = hidden + (size_t)tok[min(m0 + fr, cnt - 1)] * H + kb0 * BLK + kg * 32;
-#pragma unroll
-  for (int kk = 0; kk < D1_KPW; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) a.rows[kk][h] = *reinterpret_cast<const v4i*>(ap + kk * BLK + 16 * h);
-}
-
-__device__ __forceinline__ void g1_stage_a_store(const G1AStage& a, G1Shared& sh, int wave) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];  // lanes past 112: padding
-#pragma unroll
-  for (int kk = 0; kk < D1_KPW; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = a.rows[kk][h];
-}
 
 // Buffer loads for the prologue: a wave-uniform resource (base, byte range) in
 // SGPRs, a 32-bit offset per lane. With a range of 0 the loads return zeros
@@ -213,10 +191,11 @@ __device__ __forceinline__ void g1_load_w_pro(v8i (&b)[D1_KPW], const uint8_t* _
     b[kk] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
 }
-__device__ __forceinline__ void g1_stage_a_load_pro(G1AStage& a, const int* tok, int cnt,
+template <int NA>
+__device__ __forceinline__ void g1_stage_a_load_pro(G1AStage<NA>& a, const int* tok, int cnt,
                                                     const uint8_t* __restrict__ hidden,
                                                     const float* __restrict__ hscale, int T, int wave, bool valid) {
-  const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
+  const int lane = threadIdx.x & 63;
   const int kb0 = wave * D1_KPW;
   const __amdgpu_buffer_rsrc_t rs = buf_rsrc(hscale, valid ? (uint32_t)(NB_H * T * 4) : 0u);
 #pragma unroll
@@ -226,11 +205,26 @@ __device__ __forceinline__ void g1_stage_a_load_pro(G1AStage& a, const int* tok,
     a.sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
   }
   const __amdgpu_buffer_rsrc_t rr = buf_rsrc(hidden + kb0 * BLK, valid ? (uint32_t)(T * H) : 0u);
-  const uint32_t off = (uint32_t)(tok[max(min(fr, cnt - 1), 0)] * H + kg * 32);
 #pragma unroll
-  for (int kk = 0; kk < D1_KPW; ++kk)
+  for (int i = 0; i < NA; ++i) {
+    const int byte = 1024 * i + 16 * lane, r = byte / D1_ROW, o = byte % D1_ROW;
+    // rows at or past the count read past the range: zeros, no memory access
+    const uint32_t off = r < cnt ? (uint32_t)(tok[min(r, 15)] * H + o) : 0xFFFFFFF0u;
+    a.rows[i] = buf_load16(rr, off);
+  }
+}
+
+template <int NA>
+__device__ __forceinline__ void g1_stage_a_store(const G1AStage<NA>& a, G1Shared& sh, int wave) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) a.rows[kk][h] = buf_load16(rr, off + kk * BLK + 16 * h);
+  for (int j = 0; j < 2; ++j) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];  // lanes past 112: padding
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int byte = 1024 * i + 16 * lane, r = byte / D1_ROW, o = byte % D1_ROW;
+    const int kk = o >> 7, kg = (o >> 5) & 3, h = (o >> 4) & 1;  // r < 16: byte < 14 * 1024
+    *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][(r + 16 * kg) * 16]) = a.rows[i];
+  }
 }
 
 // The same in one step, for a change of expert or a later 16-row pass inside the
@@ -370,7 +364,6 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const int begin = blockIdx.x * per, end = min(total, begin + per);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), kb0 = wave * D1_KPW;
   G1State st;
-  G1AStage a0;
   const bool has0 = begin < end, ring = end - begin >= 5, has1 = ring || begin + 1 < end;  // uniform
   const int le0 = has0 ? nth_set_bit(act, begin / D1_NT) : 0;
   const int le1 = has1 ? nth_set_bit(act, (begin + 1) / D1_NT) : 0;
@@ -379,15 +372,25 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const int cnt0 = __popcll(m0), rank = __popcll(m0 & ((1ull << lane) - 1ull));
   if (in0 && rank < 16) sh.tok0[wave][rank] = lane;  // this wave's copy, read only by this wave
   if (lane == 0 && cnt0 == 0) sh.tok0[wave][0] = 0;  // (no item: any valid index)
-  g1_stage_a_load_pro(a0, &sh.tok0[wave][0], cnt0, hidden, hscale, T, wave, has0);
-  __builtin_amdgcn_sched_barrier(0);  // the rows are requested ahead of the weights
   v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
-  g1_load_w_pro(b0, w13, le0, begin % D1_NT, kb0, has0);
-  g1_stage_a_store(a0, sh, wave);  // waits for the rows only (requested before item 0's weights)
+  // the rows, then item 0's weights, the rows to LDS (a wait for the rows only),
+  // item 1's weights: one straight-line copy per compact load count, so that the
+  // compiler counts the requests in flight exactly on every path (the paths end
+  // alike: item 0's weights, then item 1's)
+  auto prologue = [&](auto na) {
+    G1AStage<decltype(na)::value> a0;
+    g1_stage_a_load_pro(a0, &sh.tok0[wave][0], cnt0, hidden, hscale, T, wave, has0);
+    __builtin_amdgcn_sched_barrier(0);  // the rows are requested ahead of the weights
+    g1_load_w_pro(b0, w13, le0, begin % D1_NT, kb0, has0);
+    g1_stage_a_store(a0, sh, wave);  // waits for the rows only (requested before item 0's weights)
+    g1_load_w_pro(b1, w13, le1, (begin + 1) % D1_NT, kb0, has1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (cnt0 <= 1) prologue(std::integral_constant<int, 1>{});  // uniform
+  else if (cnt0 <= 4) prologue(std::integral_constant<int, 4>{});
+  else prologue(std::integral_constant<int, 14>{});
   st.cur_le = le0;
   st.a_resident = cnt0 <= 16;
-  g1_load_w_pro(b1, w13, le1, (begin + 1) % D1_NT, kb0, has1);
-  __builtin_amdgcn_sched_barrier(0);
   dispatch_small_counts_from_masks(T, sh.d);
   dispatch_small_lists(T, offset, sh.d);
   if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
