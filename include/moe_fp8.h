@@ -10,6 +10,13 @@
  * Calls on different streams are independent when each passes its own
  * workspace; the only process-global state is per-device set-up done once
  * (the compute-unit count, kernel attributes), safe under concurrent callers.
+ *
+ * Routing ties: when equal scores straddle the top-4-group or the top-8-expert
+ * cut, the experts kept are the ones the reference keeps when it runs on the
+ * CPU (torch.topk(sorted=False) there is libstdc++'s std::nth_element, which
+ * the kernels replay). The reference run on a CUDA device breaks such ties by
+ * its own selection algorithm, which no fixture here pins: on exact ties,
+ * agreement with a CUDA-run reference is not established.
  */
 #ifndef MOE_FP8_H
 #define MOE_FP8_H
