@@ -1253,25 +1253,36 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
   // scalar loads (counted by lgkmcnt), so no wait covers the stores before them:
   // a vector load here would wait, on vmcnt, for every store in flight. Rows past
   // the valid ones read the next pairs' weights (or the workspace region after
-  // the weights), unused.
+  // the weights), unused. The stores are buffer stores through a resource per
+  // row whose range ends at the expert's last valid row, so the stores of rows
+  // past it are dropped without a branch, and each lane's address is one 32-bit
+  // offset (with 64-bit row pointers the compiler spilled, and every reload's
+  // wait also waited for the stores before it).
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const float* wp = perm_w + it.seg + it.m0 + (2 * i + wm) * 32;  // uniform
+    const int rb = it.m0 + (2 * i + wm) * 32;  // the row block's first row (uniform)
+    const float* wp = perm_w + it.seg + rb;
     float wl[16], wh[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       wl[r] = wp[8 * (r / 4) + (r % 4)];
       wh[r] = wp[8 * (r / 4) + 4 + (r % 4)];
     }
+    // lane l's row of step r is 8 (r / 4) + r % 4 (uniform) + 4 lg: each step's
+    // resource starts at its uniform row, the lane's offset adds 4 lg rows and
+    // its column
+    const uint32_t off = (uint32_t)((4 * lg * H + lr) * (int)sizeof(uint16_t));
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = it.m0 + (2 * i + wm) * 32 + 8 * (r / 4) + 4 * lg + (r % 4);
-      if (row < it.cnt) {
-        const float w = lg ? wh[r] : wl[r];
-        uint16_t* dst = partial + (size_t)(it.seg + row) * H + it.nt * Q2_BN + wn * 64 + lr;
+      const int r0 = rb + 8 * (r / 4) + (r % 4);
+      const __amdgpu_buffer_rsrc_t dst =
+          buf_rsrc(partial + (size_t)(it.seg + r0) * H + it.nt * Q2_BN + wn * 64,
+                   (uint32_t)(max(it.cnt - r0, 0) * H * (int)sizeof(uint16_t)));
+      const float w = lg ? wh[r] : wl[r];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[j * 32] = c_encode(acc[i][j][r] * w);
-      }
+      for (int j = 0; j < 2; ++j)
+        __builtin_amdgcn_raw_buffer_store_b16(c_encode(acc[i][j][r] * w), dst, off + j * 32 * (int)sizeof(uint16_t),
+                                              0, 0);
     }
   }
 }
