@@ -1452,18 +1452,17 @@ constexpr int COMBINE_THREADS = 128;
 constexpr int COMBINE_COLS = 8 * COMBINE_THREADS;  // 1024 columns per workgroup
 static_assert(H % COMBINE_COLS == 0, "the combine grid covers H");
 
-// The N pairs of slot set m (ascending slots), summed into acc.
+// The N pairs of slot set m (ascending slots; lane j of pv holds slot j's pair),
+// summed into acc.
 template <int N>
-__device__ __forceinline__ void combine_pairs(const uint16_t* __restrict__ partial, const int (&p)[TOP_K], uint32_t m,
+__device__ __forceinline__ void combine_pairs(const uint16_t* __restrict__ partial, int pv, uint32_t m,
                                               float (&acc)[8]) {
   v4i v[N];  // 8 fp16 values each
 #pragma unroll
   for (int k = 0; k < N; ++k) {
     const int slot = __builtin_ctz(m);  // uniform
     m &= m - 1u;
-    int pr = p[0];
-#pragma unroll
-    for (int j = 1; j < TOP_K; ++j) pr = slot == j ? p[j] : pr;
+    const int pr = __builtin_amdgcn_readlane(pv, slot);
     const __amdgpu_buffer_rsrc_t r = buf_rsrc(partial + (size_t)pr * H + blockIdx.y * COMBINE_COLS,
                                               COMBINE_COLS * (uint32_t)sizeof(uint16_t));
     v[k] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, threadIdx.x * 16u, 0, CPOL_NT));
@@ -1485,24 +1484,24 @@ __global__ __launch_bounds__(COMBINE_THREADS) void combine_kernel(const uint16_t
                                                                   uint16_t* __restrict__ out) {
   // workgroup (t, c): token t, columns 1024 c .. 1024 c + 1023, 8 per thread
   const int t = blockIdx.x, h = blockIdx.y * COMBINE_COLS + threadIdx.x * 8;
-  int p[TOP_K];
-  uint32_t m = 0;  // slots holding a local pair
-#pragma unroll
-  for (int j = 0; j < TOP_K; ++j) {
-    p[j] = tok_pair[(size_t)t * TOP_K + j];
-    m |= (p[j] >= 0 ? 1u : 0u) << j;
-  }
+  // The token's 8 pair slots sit in lanes 0-7 (repeated above), and each pair's
+  // index is read back with readlane at its uniform slot number. An int[8] copy
+  // indexed in a loop was placed in LDS by the compiler, whose per-thread LDS
+  // addressing reads the workgroup size from the dispatch packet: one scalar read
+  // of that packet per wave held every workgroup 3-12 us at its start.
+  const int pv = tok_pair[(size_t)t * TOP_K + (threadIdx.x & (TOP_K - 1))];
+  const uint32_t m = (uint32_t)__builtin_amdgcn_ballot_w64(pv >= 0) & ((1u << TOP_K) - 1u);  // slots with a pair
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   switch (__popc(m)) {  // uniform
     case 0: break;
-    case 1: combine_pairs<1>(partial, p, m, acc); break;
-    case 2: combine_pairs<2>(partial, p, m, acc); break;
-    case 3: combine_pairs<3>(partial, p, m, acc); break;
-    case 4: combine_pairs<4>(partial, p, m, acc); break;
-    case 5: combine_pairs<5>(partial, p, m, acc); break;
-    case 6: combine_pairs<6>(partial, p, m, acc); break;
-    case 7: combine_pairs<7>(partial, p, m, acc); break;
-    default: combine_pairs<8>(partial, p, m, acc); break;
+    case 1: combine_pairs<1>(partial, pv, m, acc); break;
+    case 2: combine_pairs<2>(partial, pv, m, acc); break;
+    case 3: combine_pairs<3>(partial, pv, m, acc); break;
+    case 4: combine_pairs<4>(partial, pv, m, acc); break;
+    case 5: combine_pairs<5>(partial, pv, m, acc); break;
+    case 6: combine_pairs<6>(partial, pv, m, acc); break;
+    case 7: combine_pairs<7>(partial, pv, m, acc); break;
+    default: combine_pairs<8>(partial, pv, m, acc); break;
   }
   v4i o;
 #pragma unroll
