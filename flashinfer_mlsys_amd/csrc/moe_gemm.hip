@@ -784,10 +784,18 @@ struct P1Ring {  // the stage layout of an NST-stage ring
 constexpr int P1_SA_OFF = P1Ring<2>::BYTES > P1Ring<3>::BYTES ? P1Ring<2>::BYTES : P1Ring<3>::BYTES;
 constexpr int P1_SA_BUF = P1_BM * 4 + 16;  // activation scales of the 256 rows, then the X1 and X2 weight scales
 constexpr int P1_LDS = P1_SA_OFF + 2 * P1_SA_BUF;
-constexpr int P1_TBM = 4, P1_TBN = 8;  // 32-item blocks: 4 row tiles x 8 column tiles
+// 32-item blocks: 4 row tiles x 8 column tiles, or 2 x 16 when no expert has more
+// than one row tile (every block then holds all column tiles of 2 experts, whose
+// activation rows its 32 workgroups share; with several row tiles per expert the
+// 4 x 8 blocks share weight tiles across row tiles instead). Measured per shape
+// (GEMM1 us, T=1024 / 8192 / skew / T=14,107): 4 x 8 147.3 / 261.2 / 736.2 /
+// 572.5, 2 x 16 140.1 / 263.1 / 745.9 / 577.3, 8 x 4 and 16 x 2 slower.
+constexpr int P1_TBM = 4, P1_TBN = 8;
+constexpr int P1_TBM1 = 2, P1_TBN1 = 16;
 static_assert(P1_BM * BLK == 4 * P1_WAVES * 1024 && P1_B_BYTES == 4 * P1_WAVES * 1024,
               "4 half fragments of each operand per wave");
-static_assert(P1_NT % P1_TBN == 0 && P1_TBM * P1_TBN == 32, "block order");
+static_assert(P1_NT % P1_TBN == 0 && P1_TBM * P1_TBN == 32 && P1_NT % P1_TBN1 == 0 && P1_TBM1 * P1_TBN1 == 32,
+              "block order");
 static_assert(P1_LDS + (int)sizeof(TileMap) <= 160 * 1024, "LDS");
 static_assert((size_t)MOE_FP8_CHUNK_TOKENS * H < (1ull << 32) && (size_t)E_LOCAL * N1 * H < (1ull << 32) &&
                   (size_t)E_LOCAL * NB_N1 * NB_H * 4 < (1ull << 32),
@@ -857,10 +865,13 @@ struct P1Item {
 };
 
 // Item of round r of this workgroup (false past the end). All values uniform.
-__device__ __forceinline__ bool p1_item(const TileMap& map, int r, int slot, int G, int total, P1Item& it) {
+// one_tile: no expert has more than one row tile (selects the 2 x 16 blocks).
+__device__ __forceinline__ bool p1_item(const TileMap& map, int r, int slot, int G, int total, bool one_tile,
+                                        P1Item& it) {
   const int i = snake_item(r, slot, G);
   if (i >= total) return false;
-  const int id = block_order_item_t<P1_TBM, P1_TBN>(i, map.total_m, P1_NT);
+  const int id = one_tile ? block_order_item_t<P1_TBM1, P1_TBN1>(i, map.total_m, P1_NT)
+                          : block_order_item_t<P1_TBM, P1_TBN>(i, map.total_m, P1_NT);
   const int k = id / P1_NT;
   int e, m0;
   tile_row<P1_BM>(map, k, e, m0);
@@ -1116,10 +1127,11 @@ __global__ __launch_bounds__(P1_THREADS, 1) void gemm1_prefill_kernel(
   x.fkind = x.w >> 2;              // 0: X1, 1: X2
   const int total = __builtin_amdgcn_readfirstlane(map.total_m) * P1_NT, G = gridDim.x;
   const int slot = xcd_remap(blockIdx.x, G);
+  const bool one_tile = __builtin_amdgcn_ballot_w64((lane < E_LOCAL ? map.cnt[lane] : 0) > P1_BM) == 0;  // uniform
 #pragma unroll 1
   for (int r = 0;; ++r) {
     P1Item ic;
-    if (!p1_item(map, r, slot, G, total, ic)) break;
+    if (!p1_item(map, r, slot, G, total, one_tile, ic)) break;
     P1Src s;
     p1_src(x, perm_tok, ic, s);
     if (x.w < 4)
