@@ -361,7 +361,11 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const uint32_t act = small_active_set(T, sh.d);
   const int total = __popc(act) * D1_NT;
   const int per = (total + gridDim.x - 1) / gridDim.x;
-  const int begin = blockIdx.x * per, end = min(total, begin + per);
+  // workgroup b runs on XCD b % 8; xcd_remap gives the 32 workgroups of one XCD
+  // consecutive runs of items (neighbouring weight rows): sweep 436.4 -> 434.4 us
+  // together with the same mapping in the decode GEMM2
+  const int wgi = (gridDim.x & 7) == 0 ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  const int begin = wgi * per, end = min(total, begin + per);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), kb0 = wave * D1_KPW;
   G1State st;
   const bool has0 = begin < end, ring = end - begin >= 5, has1 = ring || begin + 1 < end;  // uniform
@@ -560,7 +564,7 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     int T, uint16_t* __restrict__ out) {
   __shared__ G2Shared sh;
   const int tid = threadIdx.x;
-  const int c0 = blockIdx.x * D2_COLS;
+  const int c0 = xcd_remap(blockIdx.x, D2_NT) * D2_COLS;  // an XCD's 32 workgroups: neighbouring column chunks
   if (tid < E_LOCAL) {
     sh.cnt[tid] = hdr->counts[tid];
     sh.seg[tid] = hdr->seg_start[tid];
