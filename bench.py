@@ -130,11 +130,11 @@ class Runner:
     def stage_us(self, c: Case, reps: int):
         """Mean duration of each stage's kernel(s): a graph of `reps` back-to-back launches of that
         stage; None for a stage that launches nothing at this T (routing at T <= 8, which the
-        decode GEMM1 does itself; the combine at T <= 64, done inside the decode GEMM2)."""
+        decode GEMM1 does itself; the combine in the decode shape, done inside the decode GEMM2)."""
         self.call(c)
         out = []
         for s in range(4):
-            if (s == 0 and c.T <= 8) or (s == 3 and c.T <= 64):
+            if (s == 0 and c.T <= 8) or (s == 3 and c.T <= _lib.MOE_FP8_DECODE_MAX_TOKENS):
                 out.append(None)
                 continue
             g = self.graph(lambda: self.stage(c, s), reps)
@@ -462,7 +462,7 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("gemm1_decode_kernel", {}).get("hbm_bytes_per_launch")
     roofline = {
-        "kernel": "gemm1_decode_kernel (dispatch + GEMM1 + SwiGLU, T<=64; also routing for T<=8)",
+        "kernel": "gemm1_decode_kernel (dispatch + GEMM1 + SwiGLU, T<=96; also routing for T<=8)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
         "algorithmic_bytes_per_launch": round(mean_bytes), "mean_launch_us": round(mean_us, 2),

@@ -30,7 +30,8 @@ __all__ = ["kernel", "run", "route", "dispatch", "route_dispatch", "quantize_act
            "SHAPE_PREFILL"]
 
 # Expert-GEMM kernel shapes for run_shape / route_dispatch (include/moe_fp8.h MOE_SHAPE_*):
-# the decode kernels up to 64 tokens and the prefill kernels above, or the prefill kernels always.
+# the decode kernels up to MOE_FP8_DECODE_MAX_TOKENS (96) tokens and the prefill kernels above, or the
+# prefill kernels always.
 SHAPE_AUTO = 0
 SHAPE_PREFILL = 1
 

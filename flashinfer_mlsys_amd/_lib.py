@@ -20,6 +20,7 @@ MOE_ERR_HIP = -5
 MOE_ERR_ARG = -6
 MOE_ERR_NOALLOC_SIZE = -7
 MOE_FP8_NOALLOC_MAX_TOKENS = 64
+MOE_FP8_DECODE_MAX_TOKENS = 96  # MOE_SHAPE_AUTO: the decode kernels up to here
 MOE_FP8_MAX_TOKENS = 1 << 20      # the forward entry points
 MOE_FP8_MAX_TAP_TOKENS = 1 << 17  # every other entry point
 MOE_FP8_CHUNK_TOKENS = 1 << 14

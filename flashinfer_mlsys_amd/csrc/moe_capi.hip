@@ -5,6 +5,7 @@
 // synchronisation, no allocation.
 #include "moe_common.h"
 #include "moe_host.h"
+#include "moe_small_dispatch.h"
 #include "../../include/moe_fp8.h"
 
 #include <algorithm>
@@ -28,7 +29,7 @@ hipError_t launch_router_logits(const uint16_t*, const uint16_t*, int, float*, i
 hipError_t launch_router_quantize(const uint16_t*, const uint16_t*, int, float*, uint8_t*, float*, int, hipStream_t);
 hipError_t launch_gemm2_decode(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const int32_t*,
                                const float*, int, uint16_t*, hipStream_t);
-int gemm1_decode_blocks_per_cu();
+int gemm1_decode_blocks_per_cu(int T);
 hipError_t launch_gemm1_prefill(const uint8_t*, const float*, int, const uint8_t*, const float*,
                                const DispatchHeader*, const int32_t*, uint16_t*, int, hipStream_t);
 hipError_t launch_gemm2_loader(const uint16_t*, const uint8_t*, const float*, const DispatchHeader*, const float*,
@@ -39,7 +40,8 @@ hipError_t launch_combine(const uint16_t*, const int32_t*, int, uint16_t*, hipSt
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kDecodeMaxTokens = 64;        // decode shape (LDS dispatch, streaming GEMMs) up to this many tokens
+constexpr int kDecodeMaxTokens = MOE_FP8_DECODE_MAX_TOKENS;  // decode shape (LDS dispatch, streaming GEMMs)
+static_assert(kDecodeMaxTokens <= moe::SMALL_T, "the decode kernels' LDS dispatch holds SMALL_T tokens");
 constexpr int kRouteInGemm1MaxTokens = 8;   // and routing inside GEMM1 (one token per wave) up to this many
 std::atomic<int> g_cu_count[kMaxDevices];
 thread_local const char* t_last_hip_error = "no error";
@@ -91,7 +93,7 @@ struct Call {
   int offset;
   float rsf;
   uint16_t* out;
-  bool decode;  // T <= 64 and the shape is not forced to the prefill kernels
+  bool decode;  // T <= kDecodeMaxTokens and the shape is not forced to the prefill kernels
   hipStream_t stream;
   moe::DispatchHeader* hdr;
   int32_t *topk_ids, *tok_pair, *perm_tok, *chunk_counts;
@@ -171,7 +173,7 @@ hipError_t run_stage(int stage, const Call& c) {
       }
     case 1:
       if (c.decode) {
-        const int grid = std::min(max_active * (I / 8), cu_count() * gemm1_decode_blocks_per_cu());
+        const int grid = std::min(max_active * (I / 8), cu_count() * gemm1_decode_blocks_per_cu(c.T));
         return launch_gemm1_decode(c.logits, c.bias, c.rsf, c.T <= kRouteInGemm1MaxTokens, c.hidden, c.hscale, c.T,
                                    c.offset, c.w13, c.s13, c.topk_ids, c.topk_w, c.hdr, c.perm_tok, c.perm_w,
                                    c.tok_pair, c.c_act, grid, c.stream);

@@ -16,7 +16,7 @@
 // in with the weight block scale.
 //
 // Two shapes of each GEMM:
-//   *_decode  -- T <= 64, few rows per expert, weight-streaming bound. The
+//   *_decode  -- T <= 96, few rows per expert, weight-streaming bound. The
 //                waves split K, so each weight byte is read once, and the next
 //                items' weights are in flight while the current one computes;
 //                partial sums meet in LDS. GEMM1: persistent workgroups walk
@@ -92,7 +92,7 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* f) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM1 + SwiGLU, decode shape (T <= 64).
+// GEMM1 + SwiGLU, decode shape (T <= 96; built for up to 128).
 //
 // Every workgroup derives the dispatch from the routing output in its own LDS
 // (dispatch_small_*): the per-expert counts first, then the first two items'
@@ -117,11 +117,12 @@ constexpr int D1_KPW = NB_H / D1_WAVES;  // 7 K blocks per wave
 constexpr int D1_NT = I / 8;             // items per expert
 constexpr int D1_LOADS = 2 * D1_KPW;     // 16 B loads per lane for one item's weights
 static_assert(NB_H % D1_WAVES == 0, "K slices");
-static_assert(64 * D1_WAVES >= SMALL_P, "dispatch_small needs 512 threads");
+static_assert(64 * D1_WAVES >= SMALL_T, "dispatch_small: a thread per token mask");
 static_assert(D1_LOADS == 14, "the vmcnt immediates below count 14 loads per item");
 
+template <int TM>
 struct G1Shared {
-  SmallDispatch d;
+  SmallDispatch<TM> d;
   float red[2][D1_WAVES][4][64];
   __attribute__((aligned(16))) uint8_t a[D1_WAVES][D1_KPW][2][1024];  // wave's K slice, 16 rows, fragment halves
   __attribute__((aligned(16))) float sa[D1_WAVES][D1_KPW + 1][16];    // their activation scales (+16 padding)
@@ -129,9 +130,9 @@ struct G1Shared {
 };
 
 struct G1State {
-  int cur_le = -1;
-  bool a_resident = false;  // sh.a holds rows 0..15 of expert cur_le
-  int phase = 0;            // reductions done (selects the red buffer)
+  int cur_le = -1;  // sh.a holds rows a_m0 .. a_m0 + 15 of expert cur_le
+  int a_m0 = 0;
+  int phase = 0;    // reductions done (selects the red buffer)
 };
 
 __device__ __forceinline__ void g1_load_w(v8i (&b)[D1_KPW], const uint8_t* __restrict__ w13, int le, int nt, int kb0) {
@@ -214,8 +215,8 @@ __device__ __forceinline__ void g1_stage_a_load_pro(G1AStage<NA>& a, const int* 
   }
 }
 
-template <int NA>
-__device__ __forceinline__ void g1_stage_a_store(const G1AStage<NA>& a, G1Shared& sh, int wave) {
+template <int NA, class SH>
+__device__ __forceinline__ void g1_stage_a_store(const G1AStage<NA>& a, SH& sh, int wave) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < 2; ++j) (&sh.sa[wave][0][0])[lane + 64 * j] = a.sc[j];  // lanes past 112: padding
@@ -230,9 +231,10 @@ __device__ __forceinline__ void g1_stage_a_store(const G1AStage<NA>& a, G1Shared
 // The same in one step, for a change of expert or a later 16-row pass inside the
 // run: the scales by 4 B direct loads (no registers held while the weight ring is
 // full), the rows through registers; the caller waits for the direct loads.
-__device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restrict__ hidden,
+template <class SH>
+__device__ __forceinline__ void g1_stage_a(SH& sh, const uint8_t* __restrict__ hidden,
                                            const float* __restrict__ hscale, int T, int le, int m0, int wave) {
-  const SmallDispatch& d = sh.d;
+  const auto& d = sh.d;
   const int lane = threadIdx.x & 63, fr = lane & 15, kg = lane >> 4;
   const int cnt = d.cnt[le], seg = d.seg[le], kb0 = wave * D1_KPW;
 #pragma unroll
@@ -252,21 +254,99 @@ __device__ __forceinline__ void g1_stage_a(G1Shared& sh, const uint8_t* __restri
       *reinterpret_cast<v4i*>(&sh.a[wave][kk][h][lane * 16]) = *reinterpret_cast<const v4i*>(ap + kk * BLK + 16 * h);
 }
 
-template <bool PF>
-__device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i (&b2)[D1_KPW], G1State& st,
-                                        G1Shared& sh, const uint8_t* __restrict__ hidden,
-                                        const float* __restrict__ hscale, int T, const uint8_t* __restrict__ w13,
-                                        const float* __restrict__ s13, uint16_t* __restrict__ c_act) {
+// One 16-row pass of item (le, nt): rows m0 .. m0 + 15 (staged in sh.a) against
+// the item's weights b, the cross-wave reduction, SwiGLU and the C rows.
+template <class SH>
+__device__ __forceinline__ void g1_pass(int m0, int cnt, int seg, int nt, const v8i (&b)[D1_KPW],
+                                        const float (&swu)[D1_KPW], const float (&swg)[D1_KPW], G1State& st,
+                                        SH& sh, uint16_t* __restrict__ c_act) {
   const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15, kg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kk = 0; kk < D1_KPW; ++kk) {
+    const v8i a = lds_frag(&sh.a[wave][kk][0][0]);
+    const v4f p = mfma_fp8_k128(a, b[kk]);
+    const float sw = fr < 8 ? swu[kk] : swg[kk];
+    const v4f sa = *reinterpret_cast<const v4f*>(&sh.sa[wave][kk][4 * kg]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += p[r] * (sa[r] * sw);
+  }
+  float(&red)[D1_WAVES][4][64] = sh.red[st.phase & 1];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+  lds_barrier();
+  if (tid < 256) {
+    const int r = tid >> 6, ln = tid & 63;
+    if ((ln & 15) < 8) {
+      float x1 = 0.f, x2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < D1_WAVES; ++w) {
+        x1 += red[w][r][ln];
+        x2 += red[w][r][ln + 8];
+      }
+      const int row = m0 + 4 * (ln >> 4) + r;
+      if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = c_encode(silu_mul(x1, x2));
+    }
+  }
+  ++st.phase;
+}
+
+// Item (le, nt) with the weights in b; requests item + 2's weights into b2. One
+// pass per 16 rows of the expert. Loads complete in order, so a wait for rows
+// requested after item + 2's weights would wait for those weights as well: the
+// rows of every pass are staged before that request goes out, which comes just
+// before the last pass (for an expert of at most 16 rows, its only pass: after
+// the rows on a change of expert), and the waits of the earlier passes cover
+// only their rows and item + 1's weights, requested an item ago. The passes run
+// forwards and backwards on alternate items of an expert, so each item starts
+// with the rows the previous one left in LDS.
+template <bool PF, class SH>
+__device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i (&b2)[D1_KPW], G1State& st,
+                                        SH& sh, const uint8_t* __restrict__ hidden,
+                                        const float* __restrict__ hscale, int T, const uint8_t* __restrict__ w13,
+                                        const float* __restrict__ s13, uint16_t* __restrict__ c_act) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kb0 = wave * D1_KPW;
-  const SmallDispatch& d = sh.d;
+  const auto& d = sh.d;
   const int le = __builtin_amdgcn_readfirstlane(d.active[item / D1_NT]), nt = item % D1_NT;
   const int cnt = __builtin_amdgcn_readfirstlane(d.cnt[le]), seg = __builtin_amdgcn_readfirstlane(d.seg[le]);
-  const bool stage = !(st.a_resident && st.cur_le == le);  // uniform over the workgroup
+  // weight scales: the X1 block row (lanes 0-7) or the X2 block row (lanes 8-15).
+  // Both are read at wave-uniform addresses (scalar loads, counted by lgkmcnt):
+  // a per-lane vector load would make the MFMAs wait for vmcnt(0), i.e. for the
+  // prefetched weights of the next two items as well. Read before the first
+  // pass: for a one-pass item after item + 2's request.
+  const float* su = s13 + ((size_t)le * NB_N1 + (nt * 8) / BLK) * NB_H + kb0;
+  const float* sg = su + (size_t)NB_I * NB_H;
+  float swu[D1_KPW], swg[D1_KPW];
+  auto load_scales = [&] {
+#pragma unroll
+    for (int kk = 0; kk < D1_KPW; ++kk) {
+      swu[kk] = su[kk];
+      swg[kk] = sg[kk];
+    }
+  };
+  const int last = (cnt - 1) & ~15;                              // the last pass's first row
+  const bool back = last > 0 && st.cur_le == le && st.a_m0 == last;  // LDS holds the last pass
+  int held = st.cur_le == le ? st.a_m0 : -1;                     // rows in LDS (uniform)
+  if (__builtin_expect(last > 0, 0)) {  // more than 16 rows: every pass but the final one
+    load_scales();
+    for (int q = 0; q < last; q += 16) {
+      const int m0 = back ? last - q : q;
+      if (held != m0) {
+        g1_stage_a(sh, hidden, hscale, T, le, m0, wave);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      g1_pass(m0, cnt, seg, nt, b, swu, swg, st, sh, c_act);
+      held = m0;
+    }
+  }
+  const int mf = back ? 0 : last;
+  const bool stage = held != mf;
   // (the first item's rows are staged before the weight stream starts; a change
   // of expert later in the run waits here for the weights already in flight)
-  if (stage) g1_stage_a(sh, hidden, hscale, T, le, 0, wave);
+  if (stage) g1_stage_a(sh, hidden, hscale, T, le, mf, wave);
   const int n2 = item + 2;
   const bool pf = PF || n2 < end;
   if (pf) g1_load_w(b2, w13, __builtin_amdgcn_readfirstlane(d.active[n2 / D1_NT]), n2 % D1_NT, kb0);
@@ -274,60 +354,17 @@ __device__ __forceinline__ void g1_item(int item, int end, v8i (&b)[D1_KPW], v8i
     if (pf) asm volatile("s_waitcnt vmcnt(14)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  // weight scales: the X1 block row (lanes 0-7) or the X2 block row (lanes 8-15).
-  // Both are read at wave-uniform addresses (scalar loads, counted by lgkmcnt):
-  // a per-lane vector load here would make the MFMAs wait for vmcnt(0), i.e.
-  // for the prefetched weights of the next two items as well.
-  const float* su = s13 + ((size_t)le * NB_N1 + (nt * 8) / BLK) * NB_H + kb0;
-  const float* sg = su + (size_t)NB_I * NB_H;
-  float swu[D1_KPW], swg[D1_KPW];
-#pragma unroll
-  for (int kk = 0; kk < D1_KPW; ++kk) {
-    swu[kk] = su[kk];
-    swg[kk] = sg[kk];
-  }
-  for (int m0 = 0; m0 < cnt; m0 += 16) {
-    if (m0 > 0) {  // a later 16-row pass of a big expert: restage A, wait for everything
-      g1_stage_a(sh, hidden, hscale, T, le, m0, wave);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < D1_KPW; ++kk) {
-      const v8i a = lds_frag(&sh.a[wave][kk][0][0]);
-      const v4f p = mfma_fp8_k128(a, b[kk]);
-      const float sw = fr < 8 ? swu[kk] : swg[kk];
-      const v4f sa = *reinterpret_cast<const v4f*>(&sh.sa[wave][kk][4 * kg]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] += p[r] * (sa[r] * sw);
-    }
-    float(&red)[D1_WAVES][4][64] = sh.red[st.phase & 1];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
-    lds_barrier();
-    if (tid < 256) {
-      const int r = tid >> 6, ln = tid & 63;
-      if ((ln & 15) < 8) {
-        float x1 = 0.f, x2 = 0.f;
-#pragma unroll
-        for (int w = 0; w < D1_WAVES; ++w) {
-          x1 += red[w][r][ln];
-          x2 += red[w][r][ln + 8];
-        }
-        const int row = m0 + 4 * (ln >> 4) + r;
-        if (row < cnt) c_act[(size_t)(seg + row) * I + nt * 8 + (ln & 15)] = c_encode(silu_mul(x1, x2));
-      }
-    }
-    ++st.phase;
-  }
+  if (last == 0) load_scales();
+  g1_pass(mf, cnt, seg, nt, b, swu, swg, st, sh, c_act);
   st.cur_le = le;
-  st.a_resident = cnt <= 16;
+  st.a_m0 = mf;
 }
 
 // With route_here (T <= D1_WAVES) the workgroup first routes the T tokens
 // itself, wave t token t, into its LDS (workgroup 0 also stores the ids and
 // weights), instead of reading the routing kernel's output: a small decode
 // call is then two launches, not three.
+template <int TM>
 __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
     const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int route_here,
     const uint8_t* __restrict__ hidden, const float* __restrict__ hscale, int T, int offset,
@@ -335,7 +372,7 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
     float* __restrict__ topk_w, DispatchHeader* __restrict__ hdr, int32_t* __restrict__ perm_tok,
     float* __restrict__ perm_w, int32_t* __restrict__ tok_pair, uint16_t* __restrict__ c_act) {
   extern __shared__ __attribute__((aligned(16))) uint8_t g1d_lds[];
-  G1Shared& sh = *reinterpret_cast<G1Shared*>(g1d_lds);
+  G1Shared<TM>& sh = *reinterpret_cast<G1Shared<TM>*>(g1d_lds);
   const int lane = threadIdx.x & 63;
   if (route_here) {
     const int w = threadIdx.x >> 6;
@@ -371,10 +408,17 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   const bool has0 = begin < end, ring = end - begin >= 5, has1 = ring || begin + 1 < end;  // uniform
   const int le0 = has0 ? nth_set_bit(act, begin / D1_NT) : 0;
   const int le1 = has1 ? nth_set_bit(act, (begin + 1) / D1_NT) : 0;
-  const bool in0 = lane < T && ((sh.d.mask[lane] >> le0) & 1u);  // token `lane` routes to le0
-  const unsigned long long m0 = __ballot(in0);
-  const int cnt0 = __popcll(m0), rank = __popcll(m0 & ((1ull << lane) - 1ull));
-  if (in0 && rank < 16) sh.tok0[wave][rank] = lane;  // this wave's copy, read only by this wave
+  // le0's first 16 tokens, from the two token halves (token lane + 64 h routes to le0)
+  int cnt0 = 0;
+#pragma unroll
+  for (int h = 0; h < SmallDispatch<TM>::HALVES; ++h) {
+    const int t = lane + 64 * h;
+    const bool in0 = t < T && ((sh.d.mask[t] >> le0) & 1u);
+    const unsigned long long m0 = __ballot(in0);
+    const int rank = cnt0 + __popcll(m0 & ((1ull << lane) - 1ull));
+    if (in0 && rank < 16) sh.tok0[wave][rank] = t;  // this wave's copy, read only by this wave
+    cnt0 += __popcll(m0);
+  }
   if (lane == 0 && cnt0 == 0) sh.tok0[wave][0] = 0;  // (no item: any valid index)
   v8i b0[D1_KPW], b1[D1_KPW], b2[D1_KPW];
   // the rows, then item 0's weights, the rows to LDS (a wait for the rows only),
@@ -393,8 +437,8 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
   if (cnt0 <= 1) prologue(std::integral_constant<int, 1>{});  // uniform
   else if (cnt0 <= 4) prologue(std::integral_constant<int, 4>{});
   else prologue(std::integral_constant<int, 14>{});
-  st.cur_le = le0;
-  st.a_resident = cnt0 <= 16;
+  st.cur_le = le0;  // rows 0..15 of le0 are in LDS
+  st.a_m0 = 0;
   dispatch_small_counts_from_masks(T, sh.d);
   dispatch_small_lists(T, offset, sh.d);
   if (blockIdx.x == 0) store_small_dispatch(sh.d, T, hdr, perm_tok, perm_w, tok_pair);
@@ -414,7 +458,7 @@ __global__ __launch_bounds__(64 * D1_WAVES, 2) void gemm1_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2 x routing weight + the ordered combine, decode shape (T <= 64).
+// GEMM2 x routing weight + the ordered combine, decode shape (T <= 96; built for up to 128).
 //
 // Workgroup c owns output columns 28 c .. 28 c + 27 (W2 rows; 256 workgroups
 // cover H = 7168 exactly, so every workgroup streams the same weight bytes) and
@@ -443,15 +487,16 @@ constexpr int D2_LD = 2 * 2 * D2_KPW;    // 16 B weight loads per lane per item
 static_assert(H % D2_COLS == 0 && D2_NT == 256 && NB_I % D2_WAVES == 0, "tile shape");
 static_assert(D2_COLS % 4 == 0 && D2_COLS <= 32 && D2_COLS > 16, "two 16-column MFMA blocks, 4-column stores");
 
+template <int TM>
 struct G2Shared {
   int cnt[E_LOCAL];
   int seg[E_LOCAL + 1];
   int active[E_LOCAL];
   int nact;
-  float pw[SMALL_P];    // pair -> routing weight
-  int ptok[SMALL_P];    // pair -> token
+  float pw[TM * TOP_K];  // pair -> routing weight
+  int ptok[TM * TOP_K];  // pair -> token
   float red[2][D2_WAVES][2][4][64];  // lane index rotated by red_rot (bank-conflict-free reads)
-  float acc[SMALL_T][33];  // token x column accumulators (row stride 33: the rows of two tokens never share banks)
+  float acc[TM][33];  // token x column accumulators (row stride 33: the rows of two tokens never share banks)
 };
 
 // The cross-wave sum reads, per wave, 4 (column block, row) rows of red at the
@@ -490,10 +535,16 @@ __device__ __forceinline__ void g2_load_a(G2A& a, const uint16_t* __restrict__ c
 }
 
 // Item k (expert active[k]): a holds its first 16 pair rows on entry and item
-// k + 1's on return; b holds its weights; b2 receives item k + 2's weights.
-template <bool PF>
+// k + 1's on return; b holds its weights; b2 receives item k + 2's weights. An
+// expert of more than 16 rows takes a pass per 16 rows, each after the first
+// waiting for its rows and so for everything requested before them, item
+// k + 2's weights included. (Requesting those weights after the last pass's
+// rows instead, as the decode GEMM1 does, left the compiler unable to count the
+// requests in flight on the one-pass path, whose first MFMAs then waited for
+// most of them: the decode sweep 434 -> 450 us.)
+template <bool PF, class SH>
 __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b)[D2_LD], v4i (&b2)[D2_LD],
-                                        int& phase, G2Shared& sh, const uint16_t* __restrict__ c_act,
+                                        int& phase, SH& sh, const uint16_t* __restrict__ c_act,
                                         const uint8_t* __restrict__ w2, const float* __restrict__ s2) {
   const int tid = threadIdx.x, lane = tid & 63, fr = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -558,11 +609,12 @@ __device__ __forceinline__ void g2_item(int k, int nact, int c0, G2A& a, v4i (&b
   }
 }
 
+template <int TM>
 __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const DispatchHeader* __restrict__ hdr, const int32_t* __restrict__ perm_tok, const float* __restrict__ perm_w,
     int T, uint16_t* __restrict__ out) {
-  __shared__ G2Shared sh;
+  __shared__ G2Shared<TM> sh;
   const int tid = threadIdx.x;
   const int c0 = xcd_remap(blockIdx.x, D2_NT) * D2_COLS;  // an XCD's 32 workgroups: neighbouring column chunks
   if (tid < E_LOCAL) {
@@ -574,7 +626,7 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     sh.seg[E_LOCAL] = hdr->seg_start[E_LOCAL];
     sh.nact = hdr->n_active;
   }
-  for (int i = tid; i < SMALL_T * 33; i += 64 * D2_WAVES) (&sh.acc[0][0])[i] = 0.f;
+  for (int i = tid; i < TM * 33; i += 64 * D2_WAVES) (&sh.acc[0][0])[i] = 0.f;
   __syncthreads();
   const int nact = __builtin_amdgcn_readfirstlane(sh.nact);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kb0 = wave * D2_KPW;
@@ -586,9 +638,15 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
   // requested ahead of item 0's weights, then item 1's weights; the pair tables go
   // to LDS once those requests are out.
   const int P = sh.seg[E_LOCAL];
-  static_assert(SMALL_P <= 64 * D2_WAVES, "one pair per thread");
-  const float pwv = tid < P ? perm_w[tid] : 0.f;
-  const int ptv = tid < P ? perm_tok[tid] : 0;
+  constexpr int D2_PPT = (TM * TOP_K + 64 * D2_WAVES - 1) / (64 * D2_WAVES);  // pairs per thread
+  float pwv[D2_PPT];
+  int ptv[D2_PPT];
+#pragma unroll
+  for (int j = 0; j < D2_PPT; ++j) {
+    const int p = tid + 64 * D2_WAVES * j;
+    pwv[j] = p < P ? perm_w[p] : 0.f;
+    ptv[j] = p < P ? perm_tok[p] : 0;
+  }
   if (nact > 0) {
     const int le0 = __builtin_amdgcn_readfirstlane(sh.active[0]);
     g2_load_a(a, c_act, __builtin_amdgcn_readfirstlane(sh.seg[le0]), __builtin_amdgcn_readfirstlane(sh.cnt[le0]), 0,
@@ -596,9 +654,13 @@ __global__ __launch_bounds__(64 * D2_WAVES, 2) void gemm2_decode_kernel(
     g2_load_w(b0, w2, le0, c0, kb0);
   }
   if (nact > 1) g2_load_w(b1, w2, __builtin_amdgcn_readfirstlane(sh.active[1]), c0, kb0);
-  if (tid < P) {
-    sh.pw[tid] = pwv;
-    sh.ptok[tid] = ptv;
+#pragma unroll
+  for (int j = 0; j < D2_PPT; ++j) {
+    const int p = tid + 64 * D2_WAVES * j;
+    if (p < P) {
+      sh.pw[p] = pwv[j];
+      sh.ptok[p] = ptv[j];
+    }
   }
   __syncthreads();
   int k = 0;
@@ -1533,28 +1595,36 @@ __global__ __launch_bounds__(COMBINE_THREADS) void combine_kernel(const uint16_t
 // ---------------------------------------------------------------------------
 namespace moe {
 
+// The decode kernels are built for 64 and for 128 tokens (the LDS dispatch and
+// the per-token sums sized to match); a call takes the smaller one that holds T.
+template <int TM>
 static hipError_t gemm1_decode_set_lds() {
   static PerDeviceOnce<hipError_t> once;
   hipError_t e = hipErrorInvalidDevice;
-  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_decode_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(G1Shared)); },
+  once.get([] { return hipFuncSetAttribute(reinterpret_cast<const void*>(gemm1_decode_kernel<TM>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(G1Shared<TM>)); },
            e);
   return e;
 }
 
-int gemm1_decode_blocks_per_cu() {
+template <int TM>
+static int gemm1_decode_blocks_per_cu_t() {
   static PerDeviceOnce<int> once;
   int n = 1;
   once.get([] {
     int k = 0;
-    if (gemm1_decode_set_lds() != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemm1_decode_kernel, 64 * D1_WAVES, sizeof(G1Shared)) !=
-            hipSuccess ||
+    if (gemm1_decode_set_lds<TM>() != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&k, gemm1_decode_kernel<TM>, 64 * D1_WAVES,
+                                                     sizeof(G1Shared<TM>)) != hipSuccess ||
         k < 1)
       k = 1;
     return k;
   }, n);
   return n;
+}
+
+int gemm1_decode_blocks_per_cu(int T) {
+  return T <= 64 ? gemm1_decode_blocks_per_cu_t<64>() : gemm1_decode_blocks_per_cu_t<SMALL_T>();
 }
 
 hipError_t launch_gemm1_decode(const float* logits, const uint16_t* bias, float rsf, bool route_here,
@@ -1563,20 +1633,28 @@ hipError_t launch_gemm1_decode(const float* logits, const uint16_t* bias, float 
                                int32_t* perm_tok, float* perm_w, int32_t* tok_pair, uint16_t* c_act, int grid,
                                hipStream_t stream) {
   if (T <= 0 || T > SMALL_T || (route_here && T > D1_WAVES)) return hipErrorInvalidValue;
-  const hipError_t e = gemm1_decode_set_lds();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(grid), dim3(64 * D1_WAVES), sizeof(G1Shared), stream, logits, bias,
-                     rsf, route_here ? 1 : 0, hidden, hscale, T, offset, w13, s13, topk_ids, topk_w, hdr, perm_tok,
-                     perm_w, tok_pair, c_act);
-  return hipGetLastError();
+  auto launch = [&](auto tm) {
+    constexpr int TM = decltype(tm)::value;
+    const hipError_t e = gemm1_decode_set_lds<TM>();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gemm1_decode_kernel<TM>, dim3(grid), dim3(64 * D1_WAVES), sizeof(G1Shared<TM>), stream,
+                       logits, bias, rsf, route_here ? 1 : 0, hidden, hscale, T, offset, w13, s13, topk_ids, topk_w,
+                       hdr, perm_tok, perm_w, tok_pair, c_act);
+    return hipGetLastError();
+  };
+  return T <= 64 ? launch(std::integral_constant<int, 64>{}) : launch(std::integral_constant<int, SMALL_T>{});
 }
 
 hipError_t launch_gemm2_decode(const uint16_t* c_act, const uint8_t* w2, const float* s2, const DispatchHeader* hdr,
                                const int32_t* perm_tok, const float* perm_w, int T, uint16_t* out,
                                hipStream_t stream) {
   if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(D2_NT), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr, perm_tok,
-                     perm_w, T, out);
+  if (T <= 64)
+    hipLaunchKernelGGL(gemm2_decode_kernel<64>, dim3(D2_NT), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2, hdr,
+                       perm_tok, perm_w, T, out);
+  else
+    hipLaunchKernelGGL(gemm2_decode_kernel<SMALL_T>, dim3(D2_NT), dim3(64 * D2_WAVES), 0, stream, c_act, w2, s2,
+                       hdr, perm_tok, perm_w, T, out);
   return hipGetLastError();
 }
 

@@ -18,7 +18,7 @@
 //                     list of tokens that selected it): count rows (from given ids,
 //                     for the dispatch tap), then segment starts and ballot/popcount
 //                     ranks. No atomics, no host synchronisation.
-// dispatch_small_kernel -- the decode-size dispatch (T <= 64) in one workgroup.
+// dispatch_small_kernel -- the decode-size dispatch (T <= SMALL_T) in one workgroup.
 #include "moe_common.h"
 #include "moe_route_token.h"
 #include "moe_small_dispatch.h"
@@ -77,15 +77,18 @@ __global__ __launch_bounds__(64 * COUNT_ROW_TOKENS) void route_count_kernel(
   }
 }
 
-// Dispatch of up to 64 tokens in one workgroup with the same device code the
-// decode GEMM1 kernel runs in each of its workgroups (dispatch tap).
-__global__ __launch_bounds__(SMALL_P) void dispatch_small_kernel(const int32_t* __restrict__ topk_ids,
+// Dispatch of up to SMALL_T tokens in one workgroup with the same device code
+// the decode GEMM1 kernel runs in each of its workgroups (dispatch tap).
+constexpr int DISPATCH_SMALL_THREADS = 512;
+static_assert(DISPATCH_SMALL_THREADS >= SMALL_T, "a thread per token mask");
+template <int TM>
+__global__ __launch_bounds__(DISPATCH_SMALL_THREADS) void dispatch_small_kernel(const int32_t* __restrict__ topk_ids,
                                                                  const float* __restrict__ topk_w, int T, int offset,
                                                                  DispatchHeader* __restrict__ hdr,
                                                                  int32_t* __restrict__ perm_tok,
                                                                  float* __restrict__ perm_w,
                                                                  int32_t* __restrict__ tok_pair) {
-  __shared__ SmallDispatch d;
+  __shared__ SmallDispatch<TM> d;
   dispatch_small(topk_ids, topk_w, T, offset, d);
   store_small_dispatch(d, T, hdr, perm_tok, perm_w, tok_pair);
 }
@@ -129,8 +132,12 @@ hipError_t launch_dispatch_small(const int32_t* topk_ids, const float* topk_w, i
                                  DispatchHeader* hdr, int32_t* perm_tok, float* perm_w, int32_t* tok_pair,
                                  hipStream_t stream) {
   if (T <= 0 || T > SMALL_T) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(SMALL_P), 0, stream, topk_ids, topk_w, T, offset, hdr,
-                     perm_tok, perm_w, tok_pair);
+  if (T <= 64)
+    hipLaunchKernelGGL(dispatch_small_kernel<64>, dim3(1), dim3(DISPATCH_SMALL_THREADS), 0, stream, topk_ids, topk_w,
+                       T, offset, hdr, perm_tok, perm_w, tok_pair);
+  else
+    hipLaunchKernelGGL(dispatch_small_kernel<SMALL_T>, dim3(1), dim3(DISPATCH_SMALL_THREADS), 0, stream, topk_ids,
+                       topk_w, T, offset, hdr, perm_tok, perm_w, tok_pair);
   return hipGetLastError();
 }
 

@@ -1,10 +1,12 @@
-// Dispatch of up to 64 tokens inside one workgroup's LDS (reference
+// Dispatch of up to 128 tokens inside one workgroup's LDS (reference
 // moe/ref_moe.py:131-145): per local expert, the ascending list of tokens that
 // selected it, the pair weights and each (token, slot)'s pair index.
 //
-// With T <= 64 one token fits one lane, so a 32-bit local-expert mask per token
-// turns every expert's token list into one wave ballot: its popcount is the
-// expert's count and the popcount below a lane is that token's rank. Used by the
+// Tokens sit in lanes as two halves (token lane + 64 h), so a 32-bit
+// local-expert mask per token turns every expert's token list into two wave
+// ballots: their popcounts are the expert's count and the popcounts below a
+// lane (the first half's whole count before the second half) are that token's
+// rank. With T <= 64 the second half is empty and skipped. Used by the
 // decode GEMM1 kernel (each workgroup derives the dispatch itself, so no header
 // has to be read back from memory before the weight stream starts) and by the
 // dispatch tap kernel.
@@ -14,46 +16,57 @@
 
 namespace moe {
 
-constexpr int SMALL_T = 64;
-constexpr int SMALL_P = SMALL_T * TOP_K;
+constexpr int SMALL_T = 128;  // the largest token capacity (TM below: 64 or 128)
 
+// The LDS dispatch of at most TM tokens (TM / 64 halves of 64 tokens). The
+// kernels that use it are built for TM = 64 and TM = 128 and launched with the
+// smaller one that holds T, so that calls of at most 64 tokens run the
+// one-half code.
+template <int TM>
 struct SmallDispatch {
+  static_assert(TM % 64 == 0 && TM <= SMALL_T, "whole halves of 64 tokens");
+  static constexpr int HALVES = TM / 64;  // token t = lane + 64 h
+  static constexpr int P = TM * TOP_K;
   int cnt[E_LOCAL];
   int seg[E_LOCAL + 1];
   int nact;
   int active[E_LOCAL];
-  int ids[SMALL_P];    // routed global ids, [T, 8] ascending per token
-  float wts[SMALL_P];  // their routing weights
-  int tok[SMALL_P];    // pair -> token
-  float pw[SMALL_P];   // pair -> routing weight
-  int pair[SMALL_P];   // (token, slot) -> pair, -1 if the slot's expert is not local
-  uint32_t mask[SMALL_T];
+  int ids[P];    // routed global ids, [T, 8] ascending per token
+  float wts[P];  // their routing weights
+  int tok[P];    // pair -> token
+  float pw[P];   // pair -> routing weight
+  int pair[P];   // (token, slot) -> pair, -1 if the slot's expert is not local
+  uint32_t mask[TM];
 };
 
 // The phases below are called by every thread of the workgroup (blockDim.x a
-// multiple of 64 and at least SMALL_P; T <= SMALL_T) and synchronise through LDS
+// multiple of 64 and at least TM; T <= TM) and synchronise through LDS
 // only (lds_barrier), so loads in flight, such as prefetched weights, are not
 // waited for.
 //
 // Phase 1a, from the routed ids and weights already in d.ids / d.wts and visible
 // to every thread: one local-expert mask per token (bit e: local expert e).
-__device__ __forceinline__ void dispatch_small_masks(int T, int offset, SmallDispatch& d) {
+template <int TM>
+__device__ __forceinline__ void dispatch_small_masks(int T, int offset, SmallDispatch<TM>& d) {
   const int tid = threadIdx.x;
-  if (tid < SMALL_T) d.mask[tid] = 0u;
+  if (tid < TM) d.mask[tid] = 0u;
   lds_barrier();
-  if (tid < T * TOP_K) {
-    const unsigned le = (unsigned)(d.ids[tid] - offset);
-    if (le < (unsigned)E_LOCAL) atomicOr(&d.mask[tid >> 3], 1u << le);
-    d.pair[tid] = -1;
+  for (int i = tid; i < T * TOP_K; i += blockDim.x) {
+    const unsigned le = (unsigned)(d.ids[i] - offset);
+    if (le < (unsigned)E_LOCAL) atomicOr(&d.mask[i >> 3], 1u << le);
+    d.pair[i] = -1;
   }
   lds_barrier();
 }
 
 // The active local experts as a bit set, from the token masks (any wave, after
 // dispatch_small_masks; wave-uniform result).
-__device__ __forceinline__ uint32_t small_active_set(int T, const SmallDispatch& d) {
+template <int TM>
+__device__ __forceinline__ uint32_t small_active_set(int T, const SmallDispatch<TM>& d) {
   const int lane = threadIdx.x & 63;
-  uint32_t m = lane < T ? d.mask[lane] : 0u;
+  uint32_t m = 0u;
+#pragma unroll
+  for (int h = 0; h < SmallDispatch<TM>::HALVES; ++h) m |= lane + 64 * h < T ? d.mask[lane + 64 * h] : 0u;
   m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false);   // lane ^ 1
   m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false);   // lane ^ 2
   m |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false);  // half-row mirror
@@ -69,11 +82,17 @@ __device__ __forceinline__ int nth_set_bit(uint32_t set, int n) {
 }
 
 // Phase 1b: per-expert counts, segment starts and the active list.
-__device__ __forceinline__ void dispatch_small_counts_from_masks(int T, SmallDispatch& d) {
+template <int TM>
+__device__ __forceinline__ void dispatch_small_counts_from_masks(int T, SmallDispatch<TM>& d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   for (int le = wave; le < E_LOCAL; le += nw) {
-    const unsigned long long m = __ballot(lane < T && ((d.mask[lane] >> le) & 1u));
-    if (lane == 0) d.cnt[le] = __popcll(m);
+    int c = 0;
+#pragma unroll
+    for (int h = 0; h < SmallDispatch<TM>::HALVES; ++h) {
+      const int t = lane + 64 * h;
+      c += __popcll(__ballot(t < T && ((d.mask[t] >> le) & 1u)));
+    }
+    if (lane == 0) d.cnt[le] = c;
   }
   lds_barrier();
   if (wave == 0) {  // segment starts and the active list by one wave: lane e holds expert e
@@ -101,56 +120,66 @@ __device__ __forceinline__ void dispatch_small_counts_from_masks(int T, SmallDis
 
 // Phase 1 (1a + 1b): masks, counts, segment starts and the active list. Enough
 // to know which weights the workgroup will stream.
-__device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, SmallDispatch& d) {
+template <int TM>
+__device__ __forceinline__ void dispatch_small_counts_lds(int T, int offset, SmallDispatch<TM>& d) {
   dispatch_small_masks(T, offset, d);
   dispatch_small_counts_from_masks(T, d);
 }
 
 // Phase 1 from routed ids and weights in memory.
+template <int TM>
 __device__ __forceinline__ void dispatch_small_ids(const int32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                   int T, SmallDispatch& d) {
-  const int tid = threadIdx.x;
-  if (tid < T * TOP_K) {
-    d.ids[tid] = ids[tid];
-    d.wts[tid] = wts[tid];
+                                                   int T, SmallDispatch<TM>& d) {
+  for (int i = threadIdx.x; i < T * TOP_K; i += blockDim.x) {
+    d.ids[i] = ids[i];
+    d.wts[i] = wts[i];
   }
 }
+template <int TM>
 __device__ __forceinline__ void dispatch_small_counts(const int32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                      int T, int offset, SmallDispatch& d) {
+                                                      int T, int offset, SmallDispatch<TM>& d) {
   dispatch_small_ids(ids, wts, T, d);
   dispatch_small_counts_lds(T, offset, d);
 }
 
 // Phase 2: every expert's ascending token list, the pair weights and each
 // (token, slot)'s pair index.
-__device__ __forceinline__ void dispatch_small_lists(int T, int offset, SmallDispatch& d) {
+template <int TM>
+__device__ __forceinline__ void dispatch_small_lists(int T, int offset, SmallDispatch<TM>& d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const unsigned long long lt = (1ull << lane) - 1ull;
   for (int le = wave; le < E_LOCAL; le += nw) {
-    const bool has = lane < T && ((d.mask[lane] >> le) & 1u);
-    const unsigned long long m = __ballot(has);
-    if (has) {
-      const int pos = d.seg[le] + __popcll(m & lt);
-      int slot = 0;
+    int base = d.seg[le];
+    for (int h = 0; h < SmallDispatch<TM>::HALVES && 64 * h < T; ++h) {  // uniform
+      const int t = lane + 64 * h;
+      const bool has = t < T && ((d.mask[t] >> le) & 1u);
+      const unsigned long long m = __ballot(has);
+      if (has) {
+        const int pos = base + __popcll(m & lt);
+        int slot = 0;
 #pragma unroll
-      for (int j = 0; j < TOP_K; ++j) slot = d.ids[lane * TOP_K + j] == offset + le ? j : slot;
-      d.tok[pos] = lane;
-      d.pw[pos] = d.wts[lane * TOP_K + slot];
-      d.pair[lane * TOP_K + slot] = pos;
+        for (int j = 0; j < TOP_K; ++j) slot = d.ids[t * TOP_K + j] == offset + le ? j : slot;
+        d.tok[pos] = t;
+        d.pw[pos] = d.wts[t * TOP_K + slot];
+        d.pair[t * TOP_K + slot] = pos;
+      }
+      base += __popcll(m);
     }
   }
   lds_barrier();
 }
 
+template <int TM>
 __device__ __forceinline__ void dispatch_small(const int32_t* __restrict__ ids, const float* __restrict__ wts, int T,
-                                               int offset, SmallDispatch& d) {
+                                               int offset, SmallDispatch<TM>& d) {
   dispatch_small_counts(ids, wts, T, offset, d);
   dispatch_small_lists(T, offset, d);
 }
 
 // Writes the dispatch to memory in the layout of the dispatch kernels (header,
 // perm_tok, perm_w, tok_pair). Called by every thread of one workgroup.
-__device__ __forceinline__ void store_small_dispatch(const SmallDispatch& d, int T, DispatchHeader* __restrict__ hdr,
+template <int TM>
+__device__ __forceinline__ void store_small_dispatch(const SmallDispatch<TM>& d, int T, DispatchHeader* __restrict__ hdr,
                                                      int32_t* __restrict__ perm_tok, float* __restrict__ perm_w,
                                                      int32_t* __restrict__ tok_pair) {
   const int tid = threadIdx.x;

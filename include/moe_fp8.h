@@ -43,8 +43,10 @@ enum {
 
 /* Kernel shape of the expert GEMMs, for the test and benchmark entry points
  * below (moe_fp8_forward always uses MOE_SHAPE_AUTO): the decode kernels for
- * T <= 64 and the prefill kernels above (AUTO), or the prefill kernels at any T. */
+ * T <= MOE_FP8_DECODE_MAX_TOKENS and the prefill kernels above (AUTO), or the
+ * prefill kernels at any T. */
 enum { MOE_SHAPE_AUTO = 0, MOE_SHAPE_PREFILL = 1 };
+#define MOE_FP8_DECODE_MAX_TOKENS 96
 
 /* Largest T the forward entry points accept (they run calls above
  * MOE_FP8_CHUNK_TOKENS chunk by chunk), and the largest T of every other entry
@@ -137,10 +139,11 @@ int moe_fp8_forward_shape(int shape, const float* routing_logits, const uint16_t
 
 /*
  * Runs one stage of moe_fp8_forward_shape(shape, ...) with the same arguments, reading and
- * writing the workspace as the forward does: 0 = routing (+ dispatch for
- * T > 64), 1 = GEMM1 + SwiGLU (+ the in-workgroup dispatch for T <= 64),
- * 2 = GEMM2 x routing weight (+ the ordered combine for T <= 64), 3 = the
- * combine (T > 64; nothing for T <= 64). A stage's inputs must already be in
+ * writing the workspace as the forward does: 0 = routing (+ dispatch in the
+ * prefill shape), 1 = GEMM1 + SwiGLU (+ the in-workgroup dispatch in the decode
+ * shape), 2 = GEMM2 x routing weight (+ the ordered combine in the decode
+ * shape), 3 = the combine (prefill shape; nothing in the decode shape, i.e.
+ * MOE_SHAPE_AUTO with T <= MOE_FP8_DECODE_MAX_TOKENS). A stage's inputs must already be in
  * the workspace (a moe_fp8_forward with the same arguments ran on it); T at most
  * MOE_FP8_CHUNK_TOKENS (MOE_ERR_SIZE above: the forward would run chunks). No
  * reference counterpart (the reference timed its stages with torch.profiler,

@@ -36,6 +36,21 @@ def test_exports_every_declared_symbol(lib):
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover the header exactly"
 
 
+def test_header_constants_match_binding():
+    """Every plain numeric #define and enum value of the header equals the binding's constant."""
+    text = open(HEADER).read()
+    found = {}
+    for name, shift, num in re.findall(r"#define\s+(MOE_\w+)\s+(?:\(1 << (\d+)\)|(\d+))\s*$", text, re.M):
+        found[name] = 1 << int(shift) if shift else int(num)
+    for name, val in re.findall(r"\b(MOE_(?:ERR|OK|SHAPE)\w*)\s*=\s*(-?\d+)", text):
+        found[name] = int(val)
+    assert {"MOE_FP8_DECODE_MAX_TOKENS", "MOE_FP8_NOALLOC_MAX_TOKENS", "MOE_FP8_CHUNK_TOKENS",
+            "MOE_SHAPE_PREFILL", "MOE_ERR_NOALLOC_SIZE"} <= set(found)
+    for name, val in found.items():
+        assert getattr(_lib, name) == val, name
+    assert _lib.MOE_FP8_NOALLOC_MAX_TOKENS <= _lib.MOE_FP8_DECODE_MAX_TOKENS
+
+
 def test_abi_version_and_strings(lib):
     assert lib.moe_fp8_abi_version() == 3
     for code in (0, -1, -2, -3, -4, -5, -6, -7):
@@ -84,10 +99,12 @@ def test_forward_argument_errors(lib):
     ptrs[4] = FAKE + 4
     assert _fwd(lib, ptrs=ptrs) == _lib.MOE_ERR_ALIGN
     # the prefill kernels need the whole moe_fp8_workspace_size(T)
-    assert _fwd(lib, T=100, ws_bytes=lib.moe_fp8_workspace_size(100) - 1) == _lib.MOE_ERR_WORKSPACE
+    T = _lib.MOE_FP8_DECODE_MAX_TOKENS + 1
+    assert _fwd(lib, T=T, ws_bytes=lib.moe_fp8_workspace_size(T) - 1) == _lib.MOE_ERR_WORKSPACE
     assert lib.moe_fp8_forward_shape(_lib.MOE_SHAPE_PREFILL, *[FAKE] * 8, 16, 0, 2.5, FAKE, FAKE,
                                      lib.moe_fp8_workspace_size(16) - 1, None) == _lib.MOE_ERR_WORKSPACE
-    # the decode kernels (T <= 64) use no pair rows: less is enough, but not a few bytes
+    # the decode kernels (T <= MOE_FP8_DECODE_MAX_TOKENS) use no pair rows: less is enough, but not a
+    # few bytes
     assert _fwd(lib, T=16, ws_bytes=4096) == _lib.MOE_ERR_WORKSPACE
 
 

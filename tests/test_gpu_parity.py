@@ -255,7 +255,8 @@ def test_dispatch_large_synthetic(dev, T, offset):
 
 @pytest.mark.parametrize("case", ALL, indirect=True)
 def test_route_dispatch_as_forward_runs_it(case):
-    """Routing + dispatch exactly as the forward runs them (one fused kernel for T <= 64)."""
+    """Routing + dispatch exactly as the forward runs them (for T <= 96 the routing kernel and the
+    decode GEMM1's in-workgroup dispatch)."""
     ids, w, header, perm_tok, perm_w, pair = fm.route_dispatch(case.gpu[0], case.gpu[1], case.offset, case.rsf)
     _check_dispatch(case, ids, w, header, perm_tok, perm_w, pair)
     ids2, w2, _ = fm.route(case.gpu[0], case.gpu[1], case.rsf)
@@ -288,7 +289,7 @@ def test_forward_matches_reference(case):
 
 @pytest.mark.parametrize("case", ["decode_t1", "decode_t8", "t16", "decode_t64"], indirect=True)
 def test_decode_and_prefill_shapes_agree(case):
-    """T <= 64 runs the decode kernels by default; SHAPE_PREFILL forces the prefill kernels."""
+    """T <= 96 runs the decode kernels by default; SHAPE_PREFILL forces the prefill kernels."""
     a = case.forward().float()
     b = case.forward(shape=fm.SHAPE_PREFILL).float()
     ref = bf16_bits_to_f32(case.g["out_bf16"])
@@ -381,12 +382,13 @@ def test_zero_tokens(weights, dev):
 
 
 # (T, local_expert_offset, seed, routed_scaling_factor): token counts between the
-# benchmark's (3 and 9 around the in-GEMM1 routing limit of 8, 65 the first prefill
-# count, 100 and 257 partial row tiles, 513 one past a dispatch chunk of 512), other
-# offsets and a scaling factor of 1. Each seed is the first from 7000 + T whose
-# selection margins are at least 8 fp32 ulps and that routes a local pair.
-ODD_CASES = [(3, 0, 7003, 2.5), (9, 96, 7009, 2.5), (65, 224, 7065, 2.5), (100, 32, 7100, 1.0),
-             (257, 0, 7257, 2.5), (513, 160, 7513, 2.5)]
+# benchmark's (3 and 9 around the in-GEMM1 routing limit of 8; 65 in the decode
+# kernels' second half of 64 tokens, 96 their limit, 97 and 100 prefill counts;
+# 257 a partial row tile, 513 one past a dispatch chunk of 512), other offsets and
+# a scaling factor of 1. Each seed is the first from 7000 + T whose selection
+# margins are at least 8 fp32 ulps and that routes a local pair.
+ODD_CASES = [(3, 0, 7003, 2.5), (9, 96, 7009, 2.5), (65, 224, 7065, 2.5), (96, 64, 7096, 2.5),
+             (97, 128, 7097, 2.5), (100, 32, 7100, 1.0), (257, 0, 7257, 2.5), (513, 160, 7513, 2.5)]
 
 
 # Rows per local expert at the prefill kernels' edges: 16-row fragments (GEMM1),
@@ -434,17 +436,20 @@ def test_expert_row_counts_at_tile_edges_match_oracle(weights, dev, offset):
     assert_close_bf16(out, ref, f"edge counts offset={offset}")
 
 
-DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48], [2, 3, 4, 5, 6, 7, 8, 9]]
+DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48], [2, 3, 4, 5, 6, 7, 8, 9],
+                      [96], [65, 31], [3] * 32, [0] * 31 + [90], [30, 0, 31, 35]]
 
 
 @pytest.mark.parametrize("counts", DECODE_EDGE_COUNTS,
-                         ids=["64", "33-31", "17-16-15-1-0-15", "1x32", "last48", "2-to-9"])
+                         ids=["64", "33-31", "17-16-15-1-0-15", "1x32", "last48", "2-to-9", "96", "65-31", "3x32",
+                              "last90", "30-0-31-35"])
 @pytest.mark.parametrize("path", [fm.SHAPE_AUTO, fm.SHAPE_PREFILL], ids=["auto", "prefill"])
 def test_decode_row_counts_at_pass_edges_match_oracle(weights, dev, counts, path):
-    """At most 64 tokens with the local rows packed on few experts (a 64-row
-    expert, 16 / 17 / 31 / 33 rows, every expert with one row, only the last
-    expert, 2 to 9 rows: the decode GEMM2's activation loads in one, two or three
-    steps): the decode kernels' 16-row passes and the prefill kernels (forced)
+    """At most 96 tokens with the local rows packed on few experts (a 64-row or
+    96-row expert, 16 / 17 / 31 / 33 rows, every expert with one or three rows,
+    only the last expert, 2 to 9 rows: the decode GEMM2's activation loads in
+    one, two or three steps; experts whose tokens fall in both halves of 64
+    tokens): the decode kernels' 16-row passes and the prefill kernels (forced)
     both match the CPU oracle."""
     offset = 32
     lg, b = _routing_for_counts(counts, offset, 5151 + len(counts))
@@ -459,7 +464,9 @@ def test_decode_row_counts_at_pass_edges_match_oracle(weights, dev, counts, path
 
 @pytest.mark.parametrize("T,offset,seed,rsf", ODD_CASES)
 def test_odd_token_counts_match_oracle(weights, dev, T, offset, seed, rsf):
-    """Selection bit-exact and the whole output within the bar of the CPU oracle."""
+    """Selection bit-exact, the dispatch of both kernel shapes identical (the decode
+    shape's in-workgroup dispatch against the prefill shape's count and scatter
+    kernels), and the whole output within the bar of the CPU oracle."""
     _say(f"odd T={T} offset={offset} seed={seed} rsf={rsf}")
     lg, b, hs, hss = wl.make_activations(T, seed, offset)
     g, e = cpu_ref.selection_margins(lg, b)
@@ -468,6 +475,15 @@ def test_odd_token_counts_match_oracle(weights, dev, T, offset, seed, rsf):
     ids, _, _ = fm.route(gpu[0], gpu[1], rsf)
     ref_ids = cpu_ref.sorted_selection(cpu_ref.route(lg, b, rsf)[0])
     assert torch.equal(ids.cpu().long(), ref_ids)
+    da = fm.route_dispatch(gpu[0], gpu[1], offset, rsf, shape=fm.SHAPE_AUTO)
+    dp = fm.route_dispatch(gpu[0], gpu[1], offset, rsf, shape=fm.SHAPE_PREFILL)
+    P = int(da[2][:32].sum().item())
+    for k, (x, y) in enumerate(zip(da, dp)):
+        if k == 2:  # header: counts, segment starts, active count and list (the chunk counts differ)
+            x, y = x[:fm._lib.MOE_FP8_HEADER_WORDS], y[:fm._lib.MOE_FP8_HEADER_WORDS]
+        elif k in (3, 4):  # perm_tok, perm_w: the P pairs
+            x, y = x[:P], y[:P]
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32)), k
     out = fm.run(*gpu, offset, rsf).float().cpu().numpy()
     ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, rsf).float().numpy()
     assert_close_bf16(out, ref, f"T={T} offset={offset}")
