@@ -1365,14 +1365,19 @@ __device__ __forceinline__ void g2_loader_item(const uint8_t* q2_lds, int& slot,
   }
 }
 
-__global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
-    const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, uint16_t* __restrict__ partial) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
-  __shared__ TileMap map;
+// The GEMM2 kernel body for BM-row items (BM = 128, or 64 when no expert has
+// more than 64 rows: the activation waves then load half a stage's activation
+// part, 8 of their 16 load instructions, and the compute waves never have more
+// than one 32-row block each). The stage layout is the same for both.
+template <int BM>
+__device__ __forceinline__ void g2_loader_body(const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2,
+                                               const float* __restrict__ s2, const DispatchHeader* __restrict__ hdr,
+                                               const float* __restrict__ perm_w, uint16_t* __restrict__ partial,
+                                               uint8_t* q2_lds, TileMap& map) {
+  static_assert(BM == Q2_BM || BM == Q2_BM / 2, "128- or 64-row items");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  build_tile_map<Q2_BM>(hdr, map);
+  build_tile_map<BM>(hdr, map);
   const int total = __builtin_amdgcn_readfirstlane(map.total_m) * Q2_NT, G = gridDim.x;
   const int my_slot = xcd_remap(blockIdx.x, G);
 
@@ -1400,93 +1405,103 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     uint32_t lane_off[2];
 #pragma unroll
     for (int par = 0; par < 2; ++par) lane_off[par] = ld_row * row_bytes + (((lane & 7) ^ ld_row ^ par) * 16);
-    auto job_off = [&](int i) -> uint32_t {
-      return a_wave ? (uint32_t)(((2 * p + (i >> 3)) * 32 + (i & 3) * 8) * (I * 2) + ((i >> 2) & 1) * 128)
-                    : (uint32_t)((((p - 2) * 4 + (i >> 2)) * 32 + (i & 3) * 8) * I);
-    };
-    int round = -1, kb = NB_I, nreal = 0;
-    bool more = true;
-    auto next_item = [&]() -> bool {
-      const int i_next = snake_item(++round, my_slot, G);
-      if (i_next >= total) {
-        rsrc = buf_rsrc(w2, 0);
-        srsrc = buf_rsrc(s2, 0);
-        return false;
-      }
-      const int it = block_order_item(i_next, map_total_m, Q2_NT);
-      const int k = it / Q2_NT, nt = it % Q2_NT;
-      int e, m0;
-      tile_row<Q2_BM>(map, k, e, m0);
-      e = __builtin_amdgcn_readfirstlane(e);
-      m0 = __builtin_amdgcn_readfirstlane(m0);
-      const int cnt = __builtin_amdgcn_readfirstlane(map.cnt[e]), seg = __builtin_amdgcn_readfirstlane(map.seg[e]);
-      const int valid = min(Q2_BM, cnt - m0);
-      // the activation range ends at the valid rows: rows past it load as zeros
-      // (their output rows are dropped)
-      rsrc = a_wave ? buf_rsrc(c_act + (size_t)(seg + m0) * I, (uint32_t)valid * I * 2)
-                    : buf_rsrc(w2 + ((size_t)e * H + nt * Q2_BN) * I, (uint32_t)Q2_BN * I);
-      // the block scales of output column blocks 2 nt and 2 nt + 1
-      srsrc = buf_rsrc(s2 + ((size_t)e * NB_H + 2 * nt) * NB_I, 2 * NB_I * 4);
-      kb = 0;
-      return true;
-    };
-    auto load_block = [&](v4i (&buf)[W2_LJOBS], float& sv) {
-      if (kb == NB_I && more) more = next_item();
-      const int kk = more ? kb : 0;
-      // the scale first: a later load into the same register then waits for this
-      // small load alone, not for the block's data loads behind it
-      // (the order of the loads is pinned: the same in every copy of this code,
-      // so that the compiler's count of the loads in flight agrees at the loop head)
-      __builtin_amdgcn_sched_barrier(0);
-      sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, (uint32_t)(((lane & 1) * NB_I + kk) * 4), 0, 0));
-#pragma unroll
-      for (int i = 0; i < W2_LJOBS; ++i) {
+    auto run = [&](auto nj) {
+      constexpr int NJ = decltype(nj)::value;
+      const int jbase = a_wave ? p * NJ : p * W2_LJOBS;  // this wave's first job of the stage
+      // job i: 8 rows x 128 B at byte job_off(i) + lane_off[i % 2] of the tile
+      auto job_off = [&](int i) -> uint32_t {
+        const int j = jbase + i;
+        return a_wave ? (uint32_t)(((j >> 3) * 32 + (j & 3) * 8) * (I * 2) + ((j >> 2) & 1) * 128)
+                      : (uint32_t)((((p - 2) * 4 + (i >> 2)) * 32 + (i & 3) * 8) * I);
+      };
+      int round = -1, kb = NB_I, nreal = 0;
+      bool more = true;
+      auto next_item = [&]() -> bool {
+        const int i_next = snake_item(++round, my_slot, G);
+        if (i_next >= total) {
+          rsrc = buf_rsrc(w2, 0);
+          srsrc = buf_rsrc(s2, 0);
+          return false;
+        }
+        const int it = block_order_item(i_next, map_total_m, Q2_NT);
+        const int k = it / Q2_NT, nt = it % Q2_NT;
+        int e, m0;
+        tile_row<BM>(map, k, e, m0);
+        e = __builtin_amdgcn_readfirstlane(e);
+        m0 = __builtin_amdgcn_readfirstlane(m0);
+        const int cnt = __builtin_amdgcn_readfirstlane(map.cnt[e]), seg = __builtin_amdgcn_readfirstlane(map.seg[e]);
+        const int valid = min(BM, cnt - m0);
+        // the activation range ends at the valid rows: rows past it load as zeros
+        // (their output rows are dropped)
+        rsrc = a_wave ? buf_rsrc(c_act + (size_t)(seg + m0) * I, (uint32_t)valid * I * 2)
+                      : buf_rsrc(w2 + ((size_t)e * H + nt * Q2_BN) * I, (uint32_t)Q2_BN * I);
+        // the block scales of output column blocks 2 nt and 2 nt + 1
+        srsrc = buf_rsrc(s2 + ((size_t)e * NB_H + 2 * nt) * NB_I, 2 * NB_I * 4);
+        kb = 0;
+        return true;
+      };
+      auto load_block = [&](v4i (&buf)[NJ], float& sv) {
+        if (kb == NB_I && more) more = next_item();
+        const int kk = more ? kb : 0;
+        // the scale first: a later load into the same register then waits for this
+        // small load alone, not for the block's data loads behind it
+        // (the order of the loads is pinned: the same in every copy of this code,
+        // so that the compiler's count of the loads in flight agrees at the loop head)
         __builtin_amdgcn_sched_barrier(0);
-        buf[i] = __builtin_bit_cast(
-            v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off[i & 1] + job_off(i), kk * step_bytes, 0));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (more) {
-        ++kb;
-        ++nreal;
+        sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srsrc, (uint32_t)(((lane & 1) * NB_I + kk) * 4), 0, 0));
+  #pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+          __builtin_amdgcn_sched_barrier(0);
+          buf[i] = __builtin_bit_cast(
+              v4i, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off[i & 1] + job_off(i), kk * step_bytes, 0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
+          ++kb;
+          ++nreal;
+        }
+      };
+      auto store_block = [&](int g, const v4i (&buf)[NJ], float sv) {
+        uint8_t* st = q2_lds + (g & 1) * W2_STAGE;
+  #pragma unroll
+        for (int i = 0; i < NJ; ++i) {
+          const int job = jbase + i, rg = job & 3;
+          const int dst = a_wave ? ((job >> 3) * 2 + ((job >> 2) & 1)) * Q2_REG + rg * 1024
+                                 : Q2_A_BYTES + ((job - 32) >> 2) * Q2_REG + rg * 1024;
+          *reinterpret_cast<v4i*>(st + dst + 16 * lane) = buf[i];
+        }
+        if (p == W2_PWAVES - 1 && lane < 2) *reinterpret_cast<float*>(st + W2_WSCALE_OFF + 4 * lane) = sv;
+      };
+      v4i buf0[NJ], buf1[NJ];
+      float sv0, sv1;
+      load_block(buf0, sv0);
+      load_block(buf1, sv1);
+      // Two blocks per pass, every load and store unconditional (one path through
+      // the loop for the compiler's count of loads in flight). When block g + 1
+      // does not exist its store writes zeros into a slot no wave reads any more
+      // (block g - 1's, finished before barrier g), and its barrier is skipped.
+      int g = 0;
+      if (nreal > 0) {
+  #pragma unroll 1
+        do {
+          store_block(g, buf0, sv0);  // block g; its slot held block g - 2, read before the last barrier
+          load_block(buf0, sv0);      // block g + 2
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();  // block g is in its slot; block g - 1 is read
+          asm volatile("" ::: "memory");
+          store_block(g + 1, buf1, sv1);
+          load_block(buf1, sv1);  // block g + 3
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (g + 1 < nreal) __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          g += 2;
+        } while (g < nreal);
       }
     };
-    auto store_block = [&](int g, const v4i (&buf)[W2_LJOBS], float sv) {
-      uint8_t* st = q2_lds + (g & 1) * W2_STAGE;
-#pragma unroll
-      for (int i = 0; i < W2_LJOBS; ++i) {
-        const int job = p * W2_LJOBS + i, rg = job & 3;
-        const int dst = a_wave ? ((job >> 3) * 2 + ((job >> 2) & 1)) * Q2_REG + rg * 1024
-                               : Q2_A_BYTES + ((job - 32) >> 2) * Q2_REG + rg * 1024;
-        *reinterpret_cast<v4i*>(st + dst + 16 * lane) = buf[i];
-      }
-      if (p == W2_PWAVES - 1 && lane < 2) *reinterpret_cast<float*>(st + W2_WSCALE_OFF + 4 * lane) = sv;
-    };
-    v4i buf0[W2_LJOBS], buf1[W2_LJOBS];
-    float sv0, sv1;
-    load_block(buf0, sv0);
-    load_block(buf1, sv1);
-    // Two blocks per pass, every load and store unconditional (one path through
-    // the loop for the compiler's count of loads in flight). When block g + 1
-    // does not exist its store writes zeros into a slot no wave reads any more
-    // (block g - 1's, finished before barrier g), and its barrier is skipped.
-    int g = 0;
-    if (nreal > 0) {
-#pragma unroll 1
-      do {
-        store_block(g, buf0, sv0);  // block g; its slot held block g - 2, read before the last barrier
-        load_block(buf0, sv0);      // block g + 2
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();  // block g is in its slot; block g - 1 is read
-        asm volatile("" ::: "memory");
-        store_block(g + 1, buf1, sv1);
-        load_block(buf1, sv1);  // block g + 3
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (g + 1 < nreal) __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        g += 2;
-      } while (g < nreal);
-    }
+    // the activation waves load BM rows (NJ = 16: 32-row blocks 2 p and 2 p + 1;
+    // 8: block p), the W2 waves 256 rows
+    if (a_wave) run(std::integral_constant<int, W2_LJOBS * BM / Q2_BM>{});
+    else run(std::integral_constant<int, W2_LJOBS>{});
     return;
   }
 
@@ -1499,10 +1514,10 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
     const int it = block_order_item(i, map.total_m, Q2_NT);
     const int k = it / Q2_NT, nt = it % Q2_NT;
     int e, m0;
-    tile_row<Q2_BM>(map, k, e, m0);
+    tile_row<BM>(map, k, e, m0);
     const int cnt = map.cnt[e], seg = map.seg[e];
     // 32-row blocks holding valid rows; this wave's are 2 i + wm for i < ni
-    const int nb = (min(Q2_BM, cnt - m0) + 31) / 32;
+    const int nb = (min(BM, cnt - m0) + 31) / 32;
     const int ni = (nb + 1 - wm) / 2;
     const G2Item gi{m0, cnt, seg, nt};
     switch (ni) {
@@ -1511,6 +1526,18 @@ __global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
       default: g2_loader_item<2>(q2_lds, slot, wm, wn, lane, gi, perm_w, partial); break;
     }
   }
+}
+
+__global__ __launch_bounds__(W2_THREADS, 1) void gemm2_loader_kernel(
+    const uint16_t* __restrict__ c_act, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const DispatchHeader* __restrict__ hdr, const float* __restrict__ perm_w, uint16_t* __restrict__ partial) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t q2_lds[];
+  __shared__ TileMap map;
+  // 64-row items when every expert has at most 64 rows (uniform over the grid)
+  const int lane = threadIdx.x & 63;
+  const bool small = __builtin_amdgcn_ballot_w64(lane < E_LOCAL && hdr->counts[min(lane, E_LOCAL - 1)] > Q2_BM / 2) == 0;
+  if (small) g2_loader_body<Q2_BM / 2>(c_act, w2, s2, hdr, perm_w, partial, q2_lds, map);
+  else g2_loader_body<Q2_BM>(c_act, w2, s2, hdr, perm_w, partial, q2_lds, map);
 }
 
 // ---------------------------------------------------------------------------
