@@ -519,6 +519,32 @@ def test_graph_replay_matches_eager(case):
         assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
 
 
+@pytest.mark.parametrize("T,offset,seed", [(80, 96, 8080), (96, 0, 8096)])
+def test_graph_replay_matches_eager_second_half(weights, dev, T, offset, seed):
+    """The decode kernels built for 128 tokens (calls of 65 to 96 tokens) captured in
+    a HIP graph: every replay, with eager work between replays, gives the eager
+    output bit for bit, and the eager output is the oracle's within the bar."""
+    lg, b, hs, hss = wl.make_activations(T, seed, offset)
+    gpu = [t.to(dev) for t in (lg, b, hs, hss)] + list(weights[1])
+    out = torch.empty((T, 7168), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(fm.workspace_size(T), dtype=torch.uint8, device=dev)
+    fm.kernel(*gpu, offset, 2.5, out, workspace=ws)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, 2.5).float().numpy()
+    assert_close_bf16(eager.float().cpu().numpy(), ref, f"T={T} eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fm.kernel(*gpu, offset, 2.5, out, workspace=ws)
+    for i in range(3):
+        out.fill_(3.0)
+        other = fm.run(*gpu, offset, 2.5)  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+        assert torch.equal(other.view(torch.int16), eager.view(torch.int16))
+
+
 @pytest.mark.parametrize("case", ["prefill_t1024", "skew_t4096"], indirect=True)
 def test_prefill_stages_rerun_alone(case):
     """The GEMM stages launched again on their own (no routing or dispatch in
