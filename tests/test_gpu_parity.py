@@ -436,6 +436,22 @@ def test_expert_row_counts_at_tile_edges_match_oracle(weights, dev, offset):
     assert_close_bf16(out, ref, f"edge counts offset={offset}")
 
 
+@pytest.mark.parametrize("counts", [[64, 33, 64, 1, 0, 17], [65, 64, 2]], ids=["max64", "max65"])
+def test_gemm2_item_heights_match_oracle(weights, dev, counts):
+    """The prefill GEMM2 takes 64-row items when no expert has more than 64 rows
+    (experts of exactly 64 rows fill one item) and 128-row items otherwise (an
+    expert of 65 rows): both match the CPU oracle."""
+    offset = 64
+    lg, b = _routing_for_counts(counts, offset, 6161 + sum(counts))
+    T = lg.shape[0]
+    _say(f"GEMM2 item heights T={T} {counts}")
+    hs, hss = wl.quantize_1x128(wl.hidden_bf16(T, 6262 + T).to(torch.float32))
+    gpu = [t.to(dev) for t in (lg, b, hs, hss)] + list(weights[1])
+    out = fm.run_shape(fm.SHAPE_PREFILL, *gpu, offset, 2.5).float().cpu().numpy()
+    ref = cpu_ref.run(lg, b, hs, hss, *weights[0], offset, 2.5).float().numpy()
+    assert_close_bf16(out, ref, f"counts={counts}")
+
+
 DECODE_EDGE_COUNTS = [[64], [33, 31], [17, 16, 15, 1, 0, 15], [1] * 32, [0] * 31 + [48], [2, 3, 4, 5, 6, 7, 8, 9],
                       [96], [65, 31], [3] * 32, [0] * 31 + [90], [30, 0, 31, 35]]
 
